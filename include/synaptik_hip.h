@@ -1,0 +1,111 @@
+/*
+ * synaptik_hip.h - C ABI of the Synaptik MI355X (gfx950) execution backend, libsynaptik_hip.so.
+ *
+ * This is the native seam a Java `HipNativeApi` binds over the JDK 26 Foreign Function & Memory
+ * API, exactly as the Metal backend binds libsynaptik_metal
+ * (modules/backend/metal/src/main/java/io/github/pho001/synaptik/backend/metal/MetalNativeApi.java:3582-3700;
+ *  exports in modules/backend/metal/macos-arm64/src/synaptik_metal_foundation.m:1681-1770,8573,9984-10160).
+ *
+ * Conventions (same as the Metal ABI):
+ *   - every entry point returns an int32 status (SHK_HIP_STATUS_*), never throws, and NULLs its
+ *     out-pointer on entry;
+ *   - handles are opaque, owned by the caller's wrapper and released exactly once;
+ *   - calls may come from any thread; a context serializes the work it enqueues on its stream;
+ *   - a program run is synchronous: device work is complete when it returns
+ *     (docs/architecture/contracts/backend-execution.md:1658-1660).
+ * The last error message of the calling thread is available through shk_hip_last_error().
+ */
+#ifndef SYNAPTIK_HIP_H
+#define SYNAPTIK_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SHK_HIP_ABI_VERSION 1u
+
+/* Status vocabulary: 0-13 are the Metal ABI's codes with the same meaning
+ * (synaptik_metal_foundation.m:74-87, mapped to Java exceptions in MetalNativeApi.java:482-507).
+ * 14-16 are HIP additions. */
+enum {
+    SHK_HIP_STATUS_OK = 0,
+    SHK_HIP_STATUS_INVALID_ARGUMENT = 1,
+    SHK_HIP_STATUS_NO_DEVICE = 2,
+    SHK_HIP_STATUS_NO_COMMAND_QUEUE = 3,
+    SHK_HIP_STATUS_ALLOCATION_FAILED = 4,
+    SHK_HIP_STATUS_RANGE_OUT_OF_BOUNDS = 5,
+    SHK_HIP_STATUS_COPY_FAILED = 6,
+    SHK_HIP_STATUS_INTERNAL_ERROR = 7,
+    SHK_HIP_STATUS_UNSUPPORTED_SHAPE = 8,
+    SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED = 9,
+    SHK_HIP_STATUS_INCOMPATIBLE_RESOURCE = 10,
+    SHK_HIP_STATUS_EXECUTION_FAILED = 11,
+    SHK_HIP_STATUS_KERNEL_COMPILATION_FAILED = 12,
+    SHK_HIP_STATUS_UNSUPPORTED_OPERATION = 13,
+    /* a HIP runtime call failed; the message carries the hipError_t name */
+    SHK_HIP_STATUS_DEVICE_ERROR = 14,
+    /* an optimizer intermediate was not finite or an adaptive denominator / bias correction
+     * was not positive: nothing was committed (Java: ArithmeticException,
+     * TrainingParameter.java:488-525) */
+    SHK_HIP_STATUS_ARITHMETIC = 15,
+    /* a categorical target index lay outside the class extent (Java: IllegalArgumentException,
+     * CpuLossReferenceKernel.java:264) */
+    SHK_HIP_STATUS_INDEX_OUT_OF_BOUNDS = 16
+};
+
+/* ABI version; a binding refuses a library with another value
+ * (Metal: synaptik_metal_abi_version, MetalNativeApi.java:3655). */
+uint32_t shk_hip_abi_version(void);
+
+/* Copies the calling thread's last error message (NUL-terminated, truncated to capacity). */
+int32_t shk_hip_last_error(char* destination, uint64_t capacity);
+
+/* Context = one device + one stream. Replaces synaptik_metal_context_create/_release
+ * (synaptik_metal_foundation.m:1683-1708). */
+int32_t shk_hip_context_create(int32_t device_ordinal, void** out_context);
+int32_t shk_hip_context_release(void* context);
+/* Device facts for roofline reporting: compute units, peak engine clock (kHz), HBM bytes. */
+int32_t shk_hip_device_info(void* context, int32_t* out_compute_units, int32_t* out_clock_khz,
+                            uint64_t* out_memory_bytes, char* out_name, uint64_t name_capacity);
+
+/* Device buffers. Replace synaptik_metal_buffer_create/_release/_upload/_download
+ * (synaptik_metal_foundation.m:1710-1770). Uploads and downloads are synchronous. */
+int32_t shk_hip_buffer_create(void* context, uint64_t byte_size, void** out_buffer);
+/* Wraps caller-owned device memory (not freed on release). */
+int32_t shk_hip_buffer_wrap(void* context, void* device_pointer, uint64_t byte_size,
+                            void** out_buffer);
+int32_t shk_hip_buffer_release(void* buffer);
+int32_t shk_hip_buffer_upload(void* buffer, uint64_t offset, const void* source, uint64_t byte_count);
+int32_t shk_hip_buffer_download(void* buffer, uint64_t offset, void* destination, uint64_t byte_count);
+int32_t shk_hip_buffer_device_pointer(void* buffer, void** out_pointer);
+
+/* Programs: an op-list image (the HIP analogue of the Metal graph image decoded by
+ * synaptik_metal_mpsgraph_executable_create, synaptik_metal_foundation.m:8573). The program
+ * owns a device arena for its internal slots and scratch, allocated once here and reused by
+ * every run. Image layout: synaptik_amd/program.py (ProgramImage) and runtime.cpp. */
+int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_bytes,
+                               void** out_program);
+int32_t shk_hip_program_release(void* program);
+/* Runs the program once: binds in[i] / out[i] to the image's input / output slots by index,
+ * validates sizes and aliasing (INCOMPATIBLE_RESOURCE), enqueues every step, waits, and maps
+ * the device status word (ARITHMETIC, INDEX_OUT_OF_BOUNDS). Replaces
+ * synaptik_metal_mpsgraph_executable_run (synaptik_metal_foundation.m:9984-10083).
+ * Concurrent runs of one program serialize on its arena. */
+int32_t shk_hip_program_run(void* program, uint32_t input_count, void* const* inputs,
+                            uint32_t output_count, void* const* outputs);
+/* Arena bytes owned by the program (internal slots + scratch). */
+int32_t shk_hip_program_arena_bytes(void* program, uint64_t* out_bytes);
+/* Per-step device timing with HIP events on the context stream. Enabling clears the totals. */
+int32_t shk_hip_program_set_profiling(void* program, int32_t enabled);
+/* Writes min(capacity, steps) accumulated milliseconds per step and the number of profiled runs. */
+int32_t shk_hip_program_step_times(void* program, double* out_milliseconds, uint32_t capacity,
+                                   uint64_t* out_runs);
+int32_t shk_hip_program_step_count(void* program, uint32_t* out_steps);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SYNAPTIK_HIP_H */

@@ -1,0 +1,304 @@
+// Fused elementwise chains and SUM/MEAN/MAX reductions for gfx950.
+//
+// Pointwise: the reference fuses elementwise/activation chains into one generated kernel per
+// chain (CPU: CpuPointwiseGeneratedKernelTest; Metal: SynaptikPointwiseFusionKernelSource.h,
+// a runtime-generated instruction-list unit). Here one precompiled kernel interprets a short
+// register-machine program held in the kernel arguments: the opcode stream is wave-uniform, so
+// every branch is scalar and the kernel stays HBM-bound with one read per input and one write
+// per output, four elements per thread through 128-bit accesses.
+//
+// Reductions: SUM/MEAN/SUM_TO_SHAPE are exact in the reference (fixed-width limb accumulation
+// rounded once, CpuExactSumEmitter.java:4-12, CpuAggregateEmitter.java:18-20). The GPU
+// accumulates binary32 inputs in binary64 through a fixed-shape tree (wave shuffles, then LDS,
+// then a second deterministic pass) and rounds once; that equals the exactly rounded sum
+// unless the binary64 accumulation error crosses a binary32 rounding boundary. MAX follows
+// Java Math.max (NaN wins, +0.0 beats -0.0).
+#include "common.h"
+#include "kernels.h"
+#include <algorithm>
+
+namespace shk {
+namespace {
+
+enum PwOp : uint8_t {
+  PW_LOAD = 0,     // r[dst] = in[a]
+  PW_CONST = 1,    // r[dst] = imm
+  PW_ADD = 2, PW_SUB = 3, PW_MUL = 4, PW_DIV = 5,
+  PW_NEG = 6,
+  PW_RELU = 7, PW_TANH = 8, PW_SIGMOID = 9,
+  PW_EXP = 10, PW_LOG = 11,
+  PW_RELU_GRAD = 12,     // r[dst] = r[a] > 0 ? r[b] : 0          (WHERE(x > 0, g, 0))
+  PW_TANH_GRAD = 13,     // r[dst] = r[b] * (1 - r[a]*r[a])      (a = y, b = g)
+  PW_SIGMOID_GRAD = 14,  // r[dst] = (r[b] * r[a]) * (1 - r[a])  (a = y, b = g)
+  PW_GT = 15,            // r[dst] = r[a] > r[b] ? 1 : 0
+  PW_WHERE = 16,         // r[dst] = r[c] != 0 ? r[a] : r[b]
+  PW_STORE = 17,         // out[dst] = r[a]
+  PW_MAX = 18,           // Java Math.max
+  PW_SQRT = 19,
+};
+constexpr int PW_REGS = 8;
+
+__device__ __forceinline__ float pw_load(const PwParams& p, int k, int64_t row, int64_t col) {
+  switch (p.in_mode[k]) {
+    case 1: return p.in[k][col];
+    case 2: return p.in[k][row];
+    case 3: return p.in[k][0];
+    default: return p.in[k][row * p.C + col];
+  }
+}
+
+__device__ __forceinline__ void pw_exec(const PwParams& p, float (&r)[PW_REGS][4], int64_t e0,
+                                        int cnt, float (&outv)[PW_MAX_OUTPUTS][4]) {
+  for (int pc = 0; pc < p.n_instr; ++pc) {
+    const PwInstr ins = p.code[pc];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (q >= cnt) break;
+      float& d = r[ins.dst & (PW_REGS - 1)][q];
+      const float a = r[ins.a & (PW_REGS - 1)][q];
+      const float b = r[ins.b & (PW_REGS - 1)][q];
+      switch (ins.op) {
+        case PW_LOAD: {
+          const int64_t e = e0 + q;
+          const int k = ins.a % PW_MAX_INPUTS;
+          if (p.in_mode[k] == 0) {
+            d = p.in[k][e];
+          } else if (p.in_mode[k] == 3) {
+            d = p.in[k][0];
+          } else {
+            const int64_t row = e / p.C;
+            d = pw_load(p, k, row, e - row * p.C);
+          }
+          break;
+        }
+        case PW_CONST: d = ins.imm; break;
+        case PW_ADD: d = a + b; break;
+        case PW_SUB: d = a - b; break;
+        case PW_MUL: d = a * b; break;
+        case PW_DIV: d = a / b; break;
+        case PW_NEG: d = -a; break;
+        case PW_RELU: d = relu_f(a); break;
+        case PW_TANH: d = tanh_f(a); break;
+        case PW_SIGMOID: d = sigmoid_f(a); break;
+        case PW_EXP: d = (float)exp((double)a); break;
+        case PW_LOG: d = (float)log((double)a); break;
+        case PW_RELU_GRAD: d = act_grad(ACT_RELU, b, a); break;
+        case PW_TANH_GRAD: d = act_grad(ACT_TANH, b, a); break;
+        case PW_SIGMOID_GRAD: d = act_grad(ACT_SIGMOID, b, a); break;
+        case PW_GT: d = a > b ? 1.0f : 0.0f; break;
+        case PW_WHERE: d = (r[ins.c & (PW_REGS - 1)][q] != 0.0f) ? a : b; break;
+        case PW_STORE: outv[ins.dst & 1][q] = a; break;
+        case PW_MAX: d = java_max(a, b); break;
+        case PW_SQRT: d = (float)sqrt((double)a); break;
+        default: break;
+      }
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) pointwise_kernel(PwParams p) {
+  const int64_t n = p.R * p.C;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x * 4;
+  for (int64_t e0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; e0 < n; e0 += stride) {
+    const int cnt = (int)min<int64_t>(4, n - e0);
+    float r[PW_REGS][4];
+    float outv[PW_MAX_OUTPUTS][4];
+    pw_exec(p, r, e0, cnt, outv);
+    // Stores: vectorized when the group is complete and aligned.
+#pragma unroll
+    for (int o = 0; o < PW_MAX_OUTPUTS; ++o) {
+      if (p.out[o] == nullptr) continue;
+      float* dst = p.out[o] + e0;
+      if (cnt == 4 && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+        *reinterpret_cast<float4*>(dst) = make_float4(outv[o][0], outv[o][1], outv[o][2], outv[o][3]);
+      } else {
+        for (int q = 0; q < cnt; ++q) dst[q] = outv[o][q];
+      }
+    }
+  }
+}
+
+__global__ void fill_kernel(float* x, int64_t n, float v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    x[i] = v;
+}
+__global__ void fill_u32_kernel(uint32_t* x, int64_t n, uint32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    x[i] = v;
+}
+__global__ void copy_kernel(const float* __restrict__ s, float* __restrict__ d, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    d[i] = s[i];
+}
+
+// Column sums, pass 1: block (cx, ry) sums a 64-column x CHUNK-row panel; each of the 4 waves
+// walks a quarter of the rows with lanes on consecutive columns (coalesced 256 B rows).
+constexpr int CS_COLS = 64;
+constexpr int CS_ROWS = 256;  // rows per panel
+__global__ void __launch_bounds__(256) colsum_pass1(const float* __restrict__ x, double* part,
+                                                   int64_t R, int64_t N, int64_t ldx) {
+  __shared__ double lds[4][CS_COLS];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t col = (int64_t)blockIdx.x * CS_COLS + lane;
+  const int64_t r0 = (int64_t)blockIdx.y * CS_ROWS;
+  double s = 0.0;
+  if (col < N) {
+    const int64_t rend = min<int64_t>(R, r0 + CS_ROWS);
+    for (int64_t r = r0 + w; r < rend; r += 4) s += (double)x[r * ldx + col];
+  }
+  lds[w][lane] = s;
+  __syncthreads();
+  if (w == 0 && col < N)
+    part[(int64_t)blockIdx.y * N + col] = ((lds[0][lane] + lds[1][lane]) + lds[2][lane]) + lds[3][lane];
+}
+__global__ void colsum_pass2(const double* part, float* out, int64_t P, int64_t N,
+                             double divisor, int accumulate) {
+  const int64_t col = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (col >= N) return;
+  double s = 0.0;
+  for (int64_t i = 0; i < P; ++i) s += part[i * N + col];
+  float v = (float)(s / divisor);
+  if (accumulate) v = out[col] + v;
+  out[col] = v;
+}
+
+// Row reductions: one workgroup per row, binary64 accumulation for SUM/MEAN/LSE.
+template <int NT>
+__global__ void __launch_bounds__(NT) row_reduce_kernel(const float* __restrict__ x, float* out,
+                                                        int64_t C, int kind) {
+  __shared__ double dl[NT / 64];
+  __shared__ float fl[NT / 64];
+  const float* row = x + (int64_t)blockIdx.x * C;
+  if (kind == 2 || kind == 3) {
+    float m = -INFINITY;
+    for (int64_t c = threadIdx.x; c < C; c += NT) m = java_max(m, row[c]);
+    m = block_max<NT>(m, fl);
+    if (kind == 2) {
+      if (threadIdx.x == 0) out[blockIdx.x] = C == 0 ? -INFINITY : m;
+      return;
+    }
+    // LOG_SUM_EXP: shifted exponentials, one logarithm (CpuLogSumExpEmitter.java:4-9).
+    const float shift = (m == INFINITY || m == -INFINITY) ? 0.0f : m;
+    double s = 0.0;
+    for (int64_t c = threadIdx.x; c < C; c += NT) s += (double)(float)exp((double)(row[c] - shift));
+    s = block_sum<NT>(s, dl);
+    if (threadIdx.x == 0) {
+      float r;
+      if (m != m) r = m;
+      else if (m == INFINITY) r = INFINITY;
+      else r = shift + (float)log((double)(float)s);
+      out[blockIdx.x] = r;
+    }
+    return;
+  }
+  double s = 0.0;
+  for (int64_t c = threadIdx.x; c < C; c += NT) s += (double)row[c];
+  s = block_sum<NT>(s, dl);
+  if (threadIdx.x == 0) out[blockIdx.x] = kind == 1 ? (float)(s / (double)C) : (float)s;
+}
+
+// Whole-tensor reductions in two deterministic passes.
+constexpr int RA_BLOCKS = 1024;
+__global__ void __launch_bounds__(256) reduce_all_pass1(const float* __restrict__ x, int64_t n,
+                                                       int kind, double* part) {
+  __shared__ double dl[4];
+  __shared__ float fl[4];
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  if (kind == 2) {
+    float m = -INFINITY;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) m = java_max(m, x[i]);
+    m = block_max<256>(m, fl);
+    if (threadIdx.x == 0) part[blockIdx.x] = (double)m;
+    return;
+  }
+  double s = 0.0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) s += (double)x[i];
+  s = block_sum<256>(s, dl);
+  if (threadIdx.x == 0) part[blockIdx.x] = s;
+}
+__global__ void __launch_bounds__(256) reduce_all_pass2(const double* part, int P, int64_t n,
+                                                       int kind, float* out) {
+  __shared__ double dl[4];
+  __shared__ float fl[4];
+  if (kind == 2) {
+    float m = -INFINITY;
+    for (int i = threadIdx.x; i < P; i += 256) m = java_max(m, (float)part[i]);
+    m = block_max<256>(m, fl);
+    if (threadIdx.x == 0) out[0] = m;
+    return;
+  }
+  double s = 0.0;
+  for (int i = threadIdx.x; i < P; i += 256) s += part[i];
+  s = block_sum<256>(s, dl);
+  if (threadIdx.x == 0) out[0] = kind == 1 ? (float)(s / (double)n) : (float)s;
+}
+
+unsigned grid_for(int64_t n, int per_thread, int nt = 256) {
+  int64_t g = (n + (int64_t)nt * per_thread - 1) / ((int64_t)nt * per_thread);
+  if (g < 1) g = 1;
+  if (g > 65536) g = 65536;
+  return (unsigned)g;
+}
+
+}  // namespace
+
+hipError_t launch_pointwise(const PwParams& p, hipStream_t s) {
+  const int64_t n = p.R * p.C;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(pointwise_kernel, dim3(grid_for(n, 4)), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill(float* x, int64_t n, float value, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n, 4)), dim3(256), 0, s, x, n, value);
+  return hipGetLastError();
+}
+hipError_t launch_fill_u32(uint32_t* x, int64_t n, uint32_t value, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(n, 4)), dim3(256), 0, s, x, n, value);
+  return hipGetLastError();
+}
+hipError_t launch_copy(const float* src, float* dst, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(copy_kernel, dim3(grid_for(n, 4)), dim3(256), 0, s, src, dst, n);
+  return hipGetLastError();
+}
+
+int64_t colsum_partial_doubles(int64_t R, int64_t N) {
+  return ((R + CS_ROWS - 1) / CS_ROWS) * N;
+}
+hipError_t launch_colsum(const float* x, float* out, int64_t R, int64_t N, int64_t ldx,
+                         double divisor, int accumulate, double* partial, hipStream_t s) {
+  if (N <= 0) return hipSuccess;
+  const int64_t P = (R + CS_ROWS - 1) / CS_ROWS;
+  if (P > 0) {
+    dim3 g1((unsigned)((N + CS_COLS - 1) / CS_COLS), (unsigned)P);
+    hipLaunchKernelGGL(colsum_pass1, g1, dim3(256), 0, s, x, partial, R, N, ldx);
+  }
+  hipLaunchKernelGGL(colsum_pass2, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s, partial,
+                     out, P, N, divisor, accumulate);
+  return hipGetLastError();
+}
+
+hipError_t launch_row_reduce(const float* x, float* out, int64_t R, int64_t C, int kind,
+                             hipStream_t s) {
+  if (R <= 0) return hipSuccess;
+  hipLaunchKernelGGL(row_reduce_kernel<256>, dim3((unsigned)R), dim3(256), 0, s, x, out, C, kind);
+  return hipGetLastError();
+}
+
+int64_t reduce_all_partial_doubles(int64_t) { return RA_BLOCKS; }
+hipError_t launch_reduce_all(const float* x, float* out, int64_t n, int kind, double* partial,
+                             hipStream_t s) {
+  const unsigned g = (unsigned)std::min<int64_t>(RA_BLOCKS, std::max<int64_t>(1, (n + 1023) / 1024));
+  hipLaunchKernelGGL(reduce_all_pass1, dim3(g), dim3(256), 0, s, x, n, kind, partial);
+  hipLaunchKernelGGL(reduce_all_pass2, dim3(1), dim3(256), 0, s, (const double*)partial, (int)g, n,
+                     kind, out);
+  return hipGetLastError();
+}
+
+}  // namespace shk

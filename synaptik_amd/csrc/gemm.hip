@@ -1,0 +1,258 @@
+// fp32 MFMA GEMM for gfx950 (CDNA4): C = op(A) . op(B) with fused bias/activation epilogue.
+//
+// Replaces the reference's MATMUL routes for the Linear path:
+//   forward  Z = X . W^T          (TensorLinearExpressions.java:97-146)        -> transB = 1
+//   backward dX = dZ . W          (LinearAlgebraGradientRules.java:97-104)     -> NN
+//   backward dW = PERMUTE(X^T.dZ) (LayoutGradientRules.java:114), written directly as
+//            dW[out,in] = dZ^T . X                                             -> transA = 1
+// The reference contract allows a backend to reassociate an operation's reduction and use
+// FP32 FMA within one operation (docs/architecture/contracts/foundational-modules.md:423-425),
+// which is what the matrix cores do; results differ from the sequential no-FMA CPU oracle only
+// by reduction order (and are bit-identical when all partial sums are exact).
+//
+// Design (one workgroup per BM x BN output tile):
+//   * v_mfma_f32_32x32x2_f32: each wave owns a WM x WN sub-tile as (WM/32) x (WN/32)
+//     32x32 accumulator blocks (16 fp32 accumulators per lane per block).
+//   * Both operand tiles are staged through LDS in a [k][m] / [k][n] layout (m/n contiguous,
+//     padded pitch) so that every MFMA operand fetch is one conflict-light ds_read_b32 with
+//     consecutive lanes on consecutive addresses; K-contiguous global operands are transposed
+//     on the way in, M/N-contiguous ones are stored with ds_write_b128.
+//   * LDS is double buffered: the global loads of tile k+1 are issued into registers before the
+//     MFMAs of tile k, and written to the other LDS buffer afterwards (one barrier per tile).
+//   * Workgroup ids are remapped so that each of the 8 XCDs receives a contiguous, M-grouped
+//     block of output tiles: tiles that share A row-panels and B column-panels share an L2.
+#include "common.h"
+#include "kernels.h"
+#include <type_traits>
+
+namespace shk {
+namespace {
+
+template <int BM, int BN, int BK, int WM, int WN>
+struct GemmShape {
+  static constexpr int WGM = BM / WM;
+  static constexpr int WGN = BN / WN;
+  static constexpr int NT = WGM * WGN * 64;
+  static constexpr int MI = WM / 32;
+  static constexpr int NI = WN / 32;
+  static constexpr int PA = BM + 4;  // LDS pitch of the A tile (floats)
+  static constexpr int PB = BN + 4;
+};
+
+// Loads one BR x BK tile of an operand into registers and stores it into LDS as [k][r].
+//   KCONTIG: element (r, k) lives at ptr[r*ld + k]; otherwise at ptr[k*ld + r].
+//   VEC: float4 global loads (the contiguous extent and ld are multiples of 4, ptr 16B aligned).
+template <int BR, int BK, int NT, int PITCH, bool KCONTIG, bool VEC>
+struct TileLoader {
+  static constexpr int ELEMS = BR * BK;
+  static constexpr int PER_THREAD = VEC ? ELEMS / 4 / NT : ELEMS / NT;
+  static_assert(PER_THREAD >= 1, "tile too small for the workgroup");
+  static_assert(VEC ? (ELEMS / 4) % NT == 0 : ELEMS % NT == 0, "uneven tile split");
+  using Reg = typename std::conditional<VEC, float4, float>::type;
+  Reg reg[PER_THREAD];
+
+  __device__ __forceinline__ void load(const float* __restrict__ ptr, int64_t ld, int64_t r0,
+                                       int64_t k0, int64_t R, int64_t K) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int c = tid + i * NT;
+      if constexpr (VEC) {
+        int r, k;
+        if constexpr (KCONTIG) { r = c / (BK / 4); k = (c % (BK / 4)) * 4; }
+        else { k = c / (BR / 4); r = (c % (BR / 4)) * 4; }
+        const int64_t gr = r0 + r, gk = k0 + k;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (gr < R && gk < K) {
+          const float* src = KCONTIG ? ptr + gr * ld + gk : ptr + gk * ld + gr;
+          v = *reinterpret_cast<const float4*>(src);
+        }
+        reg[i] = v;
+      } else {
+        int r, k;
+        if constexpr (KCONTIG) { r = c / BK; k = c % BK; }
+        else { k = c / BR; r = c % BR; }
+        const int64_t gr = r0 + r, gk = k0 + k;
+        float v = 0.f;
+        if (gr < R && gk < K) v = KCONTIG ? ptr[gr * ld + gk] : ptr[gk * ld + gr];
+        reg[i] = v;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float* __restrict__ lds) const {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int c = tid + i * NT;
+      if constexpr (VEC) {
+        if constexpr (KCONTIG) {
+          const int r = c / (BK / 4), k = (c % (BK / 4)) * 4;
+          lds[(k + 0) * PITCH + r] = reg[i].x;
+          lds[(k + 1) * PITCH + r] = reg[i].y;
+          lds[(k + 2) * PITCH + r] = reg[i].z;
+          lds[(k + 3) * PITCH + r] = reg[i].w;
+        } else {
+          const int k = c / (BR / 4), r = (c % (BR / 4)) * 4;
+          *reinterpret_cast<float4*>(lds + k * PITCH + r) = reg[i];
+        }
+      } else {
+        int r, k;
+        if constexpr (KCONTIG) { r = c / BK; k = c % BK; }
+        else { k = c / BR; r = c % BR; }
+        lds[k * PITCH + r] = reg[i];
+      }
+    }
+  }
+};
+
+// Maps the linear workgroup id to an output tile: XCD-contiguous, then grouped along M.
+__device__ __forceinline__ void tile_of(int id, int tilesM, int tilesN, int& tm, int& tn) {
+  const int total = tilesM * tilesN;
+  if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
+  constexpr int GROUP = 8;
+  const int per_group = GROUP * tilesN;
+  const int g = id / per_group;
+  const int first = g * GROUP;
+  const int gsize = min(tilesM - first, GROUP);
+  const int in_group = id - g * per_group;
+  tm = first + in_group % gsize;
+  tn = in_group / gsize;
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VA, bool VB>
+__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
+gemm_f32_mfma(GemmParams p) {
+  using S = GemmShape<BM, BN, BK, WM, WN>;
+  constexpr int NT = S::NT, MI = S::MI, NI = S::NI, PA = S::PA, PB = S::PB;
+  __shared__ __attribute__((aligned(16))) float As[2][BK * PA];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BK * PB];
+
+  const int tilesM = (int)((p.M + BM - 1) / BM), tilesN = (int)((p.N + BN - 1) / BN);
+  int tm, tn;
+  tile_of(blockIdx.x, tilesM, tilesN, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / S::WGN, wn = wave % S::WGN;
+  const int l32 = lane & 31, half = lane >> 5;
+
+  // A tile: rows m, K-contiguous when A is [M,K] (transA = 0).
+  TileLoader<BM, BK, NT, PA, !TA, VA> la;
+  // B tile: rows n, K-contiguous when B is stored [N,K] (transB = 1).
+  TileLoader<BN, BK, NT, PB, TB, VB> lb;
+
+  floatx16 acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int nk = (int)((p.K + BK - 1) / BK);
+  if (nk > 0) {
+    la.load(p.A, p.lda, m0, 0, p.M, p.K);
+    lb.load(p.B, p.ldb, n0, 0, p.N, p.K);
+    la.store(As[0]);
+    lb.store(Bs[0]);
+    __syncthreads();
+  }
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      la.load(p.A, p.lda, m0, (int64_t)(kt + 1) * BK, p.M, p.K);
+      lb.load(p.B, p.ldb, n0, (int64_t)(kt + 1) * BK, p.N, p.K);
+    }
+    const float* a_s = As[cur] + wm * (MI * 32) + l32;
+    const float* b_s = Bs[cur] + wn * (NI * 32) + l32;
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 2) {
+      float a[MI], b[NI];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) a[i] = a_s[(kk + half) * PA + i * 32];
+#pragma unroll
+      for (int j = 0; j < NI; ++j) b[j] = b_s[(kk + half) * PB + j * 32];
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) {
+      la.store(As[cur ^ 1]);
+      lb.store(Bs[cur ^ 1]);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue. Accumulator r of a 32x32 block holds row (r/4)*8 + (lane/32)*4 + r%4,
+  // column lane%32 of that block.
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int64_t col = n0 + wn * (NI * 32) + j * 32 + l32;
+    if (col >= p.N) continue;
+    const float bias = (p.bias != nullptr) ? p.bias[col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * (MI * 32) + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+        if (row >= p.M) continue;
+        float v = acc[i][j][r];
+        if (p.mode == 0) {
+          if (p.bias != nullptr) v = v + bias;
+          v = apply_act(p.act, v);
+        } else {
+          v = act_grad(p.act, v, p.aux[row * p.ldaux + col]);
+        }
+        float* dst = p.C + row * p.ldc + col;
+        if (p.accumulate) v = *dst + v;
+        *dst = v;
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
+hipError_t launch_cfg(const GemmParams& p, bool va, bool vb, hipStream_t s) {
+  using S = GemmShape<BM, BN, BK, WM, WN>;
+  const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  dim3 grid((unsigned)tiles), block(S::NT);
+  if (va && vb)
+    hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, TA, TB, true, true>), grid, block, 0, s, p);
+  else if (va)
+    hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, TA, TB, true, false>), grid, block, 0, s, p);
+  else if (vb)
+    hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, TA, TB, false, true>), grid, block, 0, s, p);
+  else
+    hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, TA, TB, false, false>), grid, block, 0, s, p);
+  return hipGetLastError();
+}
+
+template <bool TA, bool TB>
+hipError_t launch_layout(const GemmParams& p, bool va, bool vb, hipStream_t s) {
+  const int64_t big_tiles = ((p.M + 127) / 128) * ((p.N + 127) / 128);
+  if (big_tiles >= 512) return launch_cfg<128, 128, 16, 64, 64, TA, TB>(p, va, vb, s);
+  return launch_cfg<64, 64, 16, 32, 32, TA, TB>(p, va, vb, s);
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+}  // namespace
+
+hipError_t launch_gemm(const GemmParams& p, hipStream_t s) {
+  if (p.M <= 0 || p.N <= 0) return hipSuccess;
+  // float4 loads need the contiguous extent, the leading dimension and the base aligned to 4.
+  const int64_t a_contig = p.transA ? p.M : p.K;
+  const int64_t b_contig = p.transB ? p.K : p.N;
+  const bool va = a_contig % 4 == 0 && p.lda % 4 == 0 && aligned16(p.A);
+  const bool vb = b_contig % 4 == 0 && p.ldb % 4 == 0 && aligned16(p.B);
+  if (!p.transA && !p.transB) return launch_layout<false, false>(p, va, vb, s);
+  if (!p.transA && p.transB) return launch_layout<false, true>(p, va, vb, s);
+  if (p.transA && !p.transB) return launch_layout<true, false>(p, va, vb, s);
+  return launch_layout<true, true>(p, va, vb, s);
+}
+
+}  // namespace shk

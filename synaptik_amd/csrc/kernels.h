@@ -1,0 +1,128 @@
+// Host-side launch interface of the gfx950 kernels. Every launcher validates nothing itself:
+// the program runtime (runtime.cpp) checks shapes, slot sizes and alignment before it calls
+// them, so a launcher is only ever handed operands that match the grid it builds.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace shk {
+
+// Status word bits written by kernels into the program's device status block.
+enum DeviceStatus : uint32_t {
+  DEV_OK = 0,
+  DEV_NON_FINITE = 1,       // an optimizer intermediate or candidate was not finite
+  DEV_INDEX_OUT_OF_BOUNDS = 2,  // a categorical target index lies outside the class extent
+  DEV_NOT_POSITIVE = 4,     // an adaptive bias correction or denominator was not positive
+};
+
+// C[M,N] = op(A)[M,K] . op(B)[K,N] with a fused epilogue.
+//   transA = 0: A is row-major [M,K] (K contiguous), transA = 1: A is stored [K,M].
+//   transB = 0: B is row-major [K,N] (N contiguous), transB = 1: B is stored [N,K].
+//   mode 0 (forward):  C = act(acc + bias)             (bias optional, act in Act)
+//   mode 1 (backward): C = act_grad(act, acc, aux)       (aux = activation output y)
+//   accumulate != 0:   the epilogue value is added to the existing C (gradient accumulation).
+struct GemmParams {
+  const float* A;
+  const float* B;
+  float* C;
+  const float* bias;
+  const float* aux;
+  int64_t M, N, K;
+  int64_t lda, ldb, ldc, ldaux;
+  int transA, transB;
+  int act, mode, accumulate;
+};
+hipError_t launch_gemm(const GemmParams& p, hipStream_t s);
+
+// Column sums of X[R,N] (row stride ldx) into out[N]; out = (float)(sum * scale_num / scale_den)
+// with the sum accumulated in binary64. Used for SUM_TO_SHAPE (bias gradients) and MEAN.
+// When accumulate != 0 the result is added to out.
+hipError_t launch_colsum(const float* x, float* out, int64_t R, int64_t N, int64_t ldx,
+                         double divisor, int accumulate, double* partial, hipStream_t s);
+int64_t colsum_partial_doubles(int64_t R, int64_t N);
+
+// Row reductions over the last axis of X[R,C]: kind 0 SUM, 1 MEAN, 2 MAX, 3 LOG_SUM_EXP.
+hipError_t launch_row_reduce(const float* x, float* out, int64_t R, int64_t C, int kind,
+                             hipStream_t s);
+
+// Whole-tensor reductions: kind 0 SUM, 1 MEAN, 2 MAX. Two deterministic passes through
+// `partial` (at least reduce_all_partial_doubles(n) doubles).
+hipError_t launch_reduce_all(const float* x, float* out, int64_t n, int kind, double* partial,
+                             hipStream_t s);
+int64_t reduce_all_partial_doubles(int64_t n);
+
+// Row softmax / log-softmax over the last axis with the reference's special-value classes;
+// optionally also writes the per-row log-sum-exp.
+hipError_t launch_softmax_fwd(const float* x, float* y, float* lse, int64_t R, int64_t C,
+                              int log_softmax, hipStream_t s);
+// dX = y (.) (g - sum(g (.) y)) + rowscale[r] * y   (rowscale optional: LOG_SUM_EXP cotangent
+// folded in, e.g. dm/R for a MEAN over the row LSE values; rowscale_const used if ptr null).
+hipError_t launch_softmax_bwd(const float* y, const float* g, float* dx, int64_t R, int64_t C,
+                              const float* rowscale, float rowscale_const, hipStream_t s);
+// dX = g[r] * exp(x - lse[r])  (LOG_SUM_EXP gradient) with g a per-row cotangent or constant.
+hipError_t launch_lse_bwd(const float* x, const float* lse, const float* g, float gconst,
+                          float* dx, int64_t R, int64_t C, hipStream_t s);
+
+// Mean squared error over n elements: loss = sum((p-t)^2) / n; grad = ((p-t)*2) * (g/n).
+hipError_t launch_mse(const float* p, const float* t, float* loss, float* grad, int64_t n,
+                      float g, double* partial, hipStream_t s);
+int64_t mse_partial_doubles(int64_t n);
+
+// Index categorical cross-entropy with logits [R,C], integer targets [R] (int32 or int64),
+// MEAN over non-ignored samples; grad = (softmax - onehot(clamp(t))) * (g / count).
+hipError_t launch_index_ce(const float* logits, const void* target, int target_is_64,
+                           float* loss, float* grad, int64_t R, int64_t C, int has_ignore,
+                           int64_t ignore_index, float g, double* partial, uint32_t* status,
+                           hipStream_t s);
+int64_t index_ce_partial_doubles(int64_t R);
+
+// Interpreted fused elementwise chain (see pointwise.hip for the instruction set).
+struct PwInstr {
+  uint8_t op, dst, a, b;
+  uint8_t c, pad0, pad1, pad2;
+  float imm;
+};
+constexpr int PW_MAX_INPUTS = 6;
+constexpr int PW_MAX_OUTPUTS = 2;
+constexpr int PW_MAX_INSTR = 48;
+struct PwParams {
+  const float* in[PW_MAX_INPUTS];
+  int64_t in_mode[PW_MAX_INPUTS];  // 0 full [R,C], 1 row vector [C], 2 column [R], 3 scalar
+  float* out[PW_MAX_OUTPUTS];
+  int64_t R, C;
+  int n_instr;
+  PwInstr code[PW_MAX_INSTR];
+};
+hipError_t launch_pointwise(const PwParams& p, hipStream_t s);
+
+// Multi-tensor optimizer. Each entry is one parameter tensor with its gradient and slots.
+constexpr int OPT_MAX_TENSORS = 24;
+struct OptTensor {
+  float* p;
+  const float* g;
+  float* m;
+  float* v;
+  int64_t n;
+  int64_t start;  // first element index in the concatenated domain
+};
+struct OptParams {
+  OptTensor t[OPT_MAX_TENSORS];
+  int count;
+  int64_t total;
+  int kind;        // 0 SGD, 1 Adam (coupled decay), 2 AdamW (decoupled decay)
+  int phase;       // 0 check (validate every intermediate), 1 apply (commit if status clear)
+  float lr, momentum, dampening, weight_decay;  // SGD
+  int nesterov, has_momentum_slot;
+  float beta1, beta2, eps;                       // Adam
+  const int64_t* completed_steps;  // device counter of prior successful updates
+  uint32_t* status;
+};
+hipError_t launch_optimizer(const OptParams& p, hipStream_t s);
+// Increments the completed-step counter when the status word is clear.
+hipError_t launch_step_commit(int64_t* counter, const uint32_t* status, hipStream_t s);
+
+hipError_t launch_fill(float* x, int64_t n, float value, hipStream_t s);
+hipError_t launch_fill_u32(uint32_t* x, int64_t n, uint32_t value, hipStream_t s);
+hipError_t launch_copy(const float* src, float* dst, int64_t n, hipStream_t s);
+
+}  // namespace shk

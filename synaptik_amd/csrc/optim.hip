@@ -1,0 +1,202 @@
+// Fused, transactional SGD / Adam / AdamW parameter update over many tensors in one launch.
+//
+// Arithmetic restates TrainingParameter.stageUpdate32 (SGD, momentum, dampening, Nesterov,
+// coupled weight decay; modules/training/.../TrainingParameter.java:622-672) and
+// stageAdaptive32 / stageAdaptiveElement32 (Adam with coupled decay, AdamW with decoupled
+// decay; TrainingParameter.java:433-525) operation by operation in binary32, with the same
+// finiteness checks on every intermediate and candidate.
+//
+// The reference stages candidates on the host and commits them only if every element of every
+// parameter passed its checks. On the device this is two streaming phases:
+//   phase 0 (check): recompute every intermediate, OR DEV_NON_FINITE / DEV_NOT_POSITIVE into the
+//                    program status word; nothing is written to parameters or slots;
+//   phase 1 (apply): if the status word is clear, recompute and store parameter and slots.
+// A failed step therefore leaves parameters and optimizer slots bit-for-bit unchanged, and the
+// completed-step counter is advanced only by launch_step_commit when the status stays clear.
+// Traffic: check reads p,g,m(,v); apply reads p,g,m(,v) and writes p,m(,v).
+#include "common.h"
+#include "kernels.h"
+
+namespace shk {
+namespace {
+
+constexpr int OPT_NT = 256;
+constexpr int OPT_PER_THREAD = 4;
+constexpr int64_t OPT_CHUNK = OPT_NT * OPT_PER_THREAD;
+
+struct Coeffs {
+  float c1, c2, decay_factor;
+  bool ok;
+};
+
+__device__ __forceinline__ Coeffs adam_coeffs(const OptParams& p, int64_t step) {
+  Coeffs k;
+  k.c1 = 1.0f - (float)pow((double)p.beta1, (double)step);
+  k.c2 = 1.0f - (float)pow((double)p.beta2, (double)step);
+  k.ok = is_finite(k.c1) && k.c1 > 0.0f && is_finite(k.c2) && k.c2 > 0.0f;
+  k.decay_factor = 1.0f;
+  if (p.kind == 2) {
+    const float scale = p.lr * p.weight_decay;
+    k.ok = k.ok && is_finite(scale);
+    k.decay_factor = k.decay_factor - scale;
+    k.ok = k.ok && is_finite(k.decay_factor);
+  }
+  return k;
+}
+
+// One SGD element. Returns false if any intermediate is not finite.
+__device__ __forceinline__ bool sgd_element(const OptParams& p, bool first, float pv, float g,
+                                            float mv, float& pc, float& mc) {
+  bool ok = is_finite(pv);
+  const float decay_term = p.weight_decay * pv;
+  ok &= is_finite(decay_term);
+  const float adjusted = g + decay_term;
+  ok &= is_finite(adjusted);
+  float selected = adjusted;
+  mc = mv;
+  if (p.momentum != 0.0f) {
+    float um;
+    if (first) {
+      um = adjusted;
+    } else {
+      const float mt = p.momentum * mv;
+      ok &= is_finite(mt);
+      const float dg = (1.0f - p.dampening) * adjusted;
+      ok &= is_finite(dg);
+      um = mt + dg;
+    }
+    ok &= is_finite(um);
+    mc = um;
+    if (p.nesterov) {
+      const float look = p.momentum * um;
+      ok &= is_finite(look);
+      selected = adjusted + look;
+      ok &= is_finite(selected);
+    } else {
+      selected = um;
+    }
+  } else if (p.has_momentum_slot) {
+    mc = 0.0f;
+  }
+  const float scaled = p.lr * selected;
+  ok &= is_finite(scaled);
+  pc = pv - scaled;
+  ok &= is_finite(pc);
+  return ok;
+}
+
+// One Adam/AdamW element.
+__device__ __forceinline__ bool adam_element(const OptParams& p, const Coeffs& k, float pv,
+                                             float g0, float mv, float vv, float& pc, float& mc,
+                                             float& vc) {
+  bool ok = is_finite(pv);
+  float gradient, base;
+  if (p.kind == 2) {
+    base = pv * k.decay_factor;
+    ok &= is_finite(base);
+    gradient = g0;
+  } else {
+    const float decay_term = p.weight_decay * pv;
+    ok &= is_finite(decay_term);
+    gradient = g0 + decay_term;
+    ok &= is_finite(gradient);
+    base = pv;
+  }
+  const float first_term = p.beta1 * mv;
+  ok &= is_finite(first_term);
+  const float first_grad = (1.0f - p.beta1) * gradient;
+  ok &= is_finite(first_grad);
+  const float first = first_term + first_grad;
+  ok &= is_finite(first);
+  const float squared = gradient * gradient;
+  ok &= is_finite(squared);
+  const float second_term = p.beta2 * vv;
+  ok &= is_finite(second_term);
+  const float second_grad = (1.0f - p.beta2) * squared;
+  ok &= is_finite(second_grad);
+  const float second = second_term + second_grad;
+  ok &= is_finite(second);
+  const float cf = first / k.c1;
+  const float cs = second / k.c2;
+  ok &= is_finite(cf) && is_finite(cs);
+  const float root = (float)sqrt((double)cs);
+  ok &= is_finite(root);
+  const float denom = root + p.eps;
+  ok &= is_finite(denom) && denom > 0.0f;
+  const float numer = p.lr * cf;
+  ok &= is_finite(numer);
+  const float update = numer / denom;
+  ok &= is_finite(update);
+  pc = base - update;
+  ok &= is_finite(pc);
+  mc = first;
+  vc = second;
+  return ok;
+}
+
+__global__ void __launch_bounds__(OPT_NT) optimizer_kernel(OptParams p) {
+  // Tensor of this block: the table holds each tensor's first block index in `start`.
+  int t = 0;
+  for (int i = 1; i < p.count; ++i)
+    if ((int64_t)blockIdx.x >= p.t[i].start) t = i;
+  const OptTensor T = p.t[t];
+  if (p.phase == 1 && *(volatile const uint32_t*)p.status != 0u) return;
+  const int64_t completed = *p.completed_steps;
+  const bool first = completed == 0;
+  Coeffs k{1.0f, 1.0f, 1.0f, true};
+  if (p.kind != 0) k = adam_coeffs(p, completed + 1);
+  const int64_t base = ((int64_t)blockIdx.x - T.start) * OPT_CHUNK;
+  bool ok = k.ok;
+  if (!k.ok && p.phase == 1) return;
+#pragma unroll
+  for (int q = 0; q < OPT_PER_THREAD; ++q) {
+    const int64_t i = base + q * OPT_NT + threadIdx.x;
+    if (i >= T.n) break;
+    const float pv = T.p[i];
+    const float g = T.g[i];
+    const float mv = T.m != nullptr ? T.m[i] : 0.0f;
+    float pc, mc, vc = 0.0f;
+    bool e;
+    if (p.kind == 0) {
+      e = sgd_element(p, first, pv, g, mv, pc, mc);
+    } else {
+      e = adam_element(p, k, pv, g, mv, T.v[i], pc, mc, vc);
+    }
+    ok &= e;
+    if (p.phase == 1) {
+      T.p[i] = pc;
+      if (T.m != nullptr) T.m[i] = mc;
+      if (p.kind != 0) T.v[i] = vc;
+    }
+  }
+  if (p.phase == 0) {
+    const int bad = wave_or(ok ? 0 : 1);
+    if (bad && (threadIdx.x & 63) == 0)
+      atomicOr(p.status, k.ok ? (uint32_t)DEV_NON_FINITE : (uint32_t)DEV_NOT_POSITIVE);
+  }
+}
+
+__global__ void step_commit_kernel(int64_t* counter, const uint32_t* status) {
+  if (threadIdx.x == 0 && blockIdx.x == 0 && *status == 0u) *counter = *counter + 1;
+}
+
+}  // namespace
+
+hipError_t launch_optimizer(const OptParams& in, hipStream_t s) {
+  OptParams p = in;
+  int64_t blocks = 0;
+  for (int i = 0; i < p.count; ++i) {
+    p.t[i].start = blocks;
+    blocks += (p.t[i].n + OPT_CHUNK - 1) / OPT_CHUNK;
+  }
+  if (blocks == 0) return hipSuccess;
+  hipLaunchKernelGGL(optimizer_kernel, dim3((unsigned)blocks), dim3(OPT_NT), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_step_commit(int64_t* counter, const uint32_t* status, hipStream_t s) {
+  hipLaunchKernelGGL(step_commit_kernel, dim3(1), dim3(64), 0, s, counter, status);
+  return hipGetLastError();
+}
+
+}  // namespace shk

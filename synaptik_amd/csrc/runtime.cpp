@@ -1,0 +1,927 @@
+// C-ABI runtime of libsynaptik_hip.so: contexts, device buffers and op-list programs.
+//
+// Shape follows the reference's Metal native bridge (synaptik_metal_foundation.m:1681-1770 for
+// context/buffers, :8573 and :9984-10083 for executable create/run): int32 status codes, opaque
+// handles, out-pointers cleared on entry, no exception crosses the ABI.
+//
+// A program is decoded and validated once at create time (every step's operand extents are
+// checked against its slots' byte sizes, so no launch can address outside a bound buffer),
+// allocates one device arena for internal slots and reduction scratch, and is then run any
+// number of times with caller-bound input/output buffers (inputs of kind INOUT are parameters and
+// optimizer slots that the program updates in place).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/synaptik_hip.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int32_t fail(int32_t status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return status;
+}
+
+#define HIP_TRY(expr)                                                                         \
+  do {                                                                                        \
+    hipError_t e_ = (expr);                                                                   \
+    if (e_ != hipSuccess)                                                                     \
+      return fail(SHK_HIP_STATUS_DEVICE_ERROR, "%s failed: %s", #expr, hipGetErrorName(e_));  \
+  } while (0)
+
+constexpr uint32_t kContextMagic = 0x43484B53u;  // "SKHC"
+constexpr uint32_t kBufferMagic = 0x42484B53u;
+constexpr uint32_t kProgramMagic = 0x50484B53u;
+constexpr uint32_t kImageMagic = 0x504B4853u;    // "SHKP" little-endian
+constexpr uint32_t kImageVersion = 1u;
+
+struct Context {
+  uint32_t magic = kContextMagic;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  uint32_t* host_status = nullptr;  // pinned
+  std::mutex mutex;
+};
+
+struct Buffer {
+  uint32_t magic = kBufferMagic;
+  Context* ctx = nullptr;
+  void* ptr = nullptr;
+  uint64_t bytes = 0;
+  bool owned = true;
+};
+
+enum SlotKind : uint32_t { SLOT_INTERNAL = 0, SLOT_INPUT = 1, SLOT_OUTPUT = 2, SLOT_INOUT = 3 };
+enum DType : uint32_t { DT_F32 = 0, DT_I32 = 1, DT_I64 = 2, DT_U8 = 3, DT_F64 = 4 };
+
+enum Opcode : uint32_t {
+  OP_GEMM = 1,
+  OP_COLSUM = 2,
+  OP_ROW_REDUCE = 3,
+  OP_REDUCE_ALL = 4,
+  OP_POINTWISE = 5,
+  OP_SOFTMAX = 6,
+  OP_SOFTMAX_BWD = 7,
+  OP_LSE_BWD = 8,
+  OP_MSE = 9,
+  OP_CE_INDEX = 10,
+  OP_OPTIMIZER = 11,
+  OP_STEP_COMMIT = 12,
+  OP_FILL = 13,
+  OP_COPY = 14,
+};
+
+#pragma pack(push, 1)
+struct ImageHeader {
+  uint32_t magic, version, n_slots, n_steps;
+};
+struct SlotRecord {
+  uint64_t bytes;
+  uint32_t kind, ext_index, dtype, flags;
+};
+struct StepRecord {
+  uint32_t opcode, payload_bytes;
+  int32_t slot[8];
+  int64_t iarg[16];
+  float farg[8];
+};
+struct OptEntry {
+  int32_t p, g, m, v;
+  int64_t n;
+};
+#pragma pack(pop)
+static_assert(sizeof(SlotRecord) == 24, "slot record layout");
+static_assert(sizeof(StepRecord) == 200, "step record layout");
+static_assert(sizeof(OptEntry) == 24, "optimizer entry layout");
+static_assert(sizeof(shk::PwInstr) == 12, "pointwise instruction layout");
+
+struct Step {
+  StepRecord rec;
+  std::vector<uint8_t> payload;
+};
+
+struct Program {
+  uint32_t magic = kProgramMagic;
+  Context* ctx = nullptr;
+  std::vector<SlotRecord> slots;
+  std::vector<Step> steps;
+  uint32_t n_inputs = 0, n_outputs = 0;
+  void* arena = nullptr;
+  uint64_t arena_bytes = 0;
+  std::vector<uint64_t> internal_offset;  // per slot (internal only)
+  double* scratch = nullptr;              // reduction partials
+  uint32_t* status = nullptr;             // device status word (inside the arena)
+  std::mutex run_mutex;
+  bool profiling = false;
+  uint64_t profiled_runs = 0;
+  std::vector<double> step_ms;
+  std::vector<hipEvent_t> events;
+};
+
+template <typename T, uint32_t M>
+T* checked(void* h) {
+  if (h == nullptr) return nullptr;
+  T* t = static_cast<T*>(h);
+  return t->magic == M ? t : nullptr;
+}
+
+uint64_t dtype_size(uint32_t dt) {
+  switch (dt) {
+    case DT_F32: case DT_I32: return 4;
+    case DT_I64: case DT_F64: return 8;
+    case DT_U8: return 1;
+    default: return 0;
+  }
+}
+
+// ---- create-time validation helpers ----
+struct Validator {
+  const std::vector<SlotRecord>& slots;
+  size_t step;
+  int32_t err = SHK_HIP_STATUS_OK;
+
+  bool slot_ok(int32_t s, bool optional, const char* role) {
+    if (s < 0) {
+      if (optional) return true;
+      err = fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: missing %s slot", step, role);
+      return false;
+    }
+    if ((size_t)s >= slots.size()) {
+      err = fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: %s slot %d out of range",
+                 step, role, s);
+      return false;
+    }
+    return true;
+  }
+  // Requires that slot s holds at least `elems` elements of dtype dt.
+  bool holds(int32_t s, int64_t elems, uint32_t dt, const char* role) {
+    if (s < 0) return true;
+    if (elems < 0) {
+      err = fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: negative extent for %s", step, role);
+      return false;
+    }
+    if (slots[s].dtype != dt) {
+      err = fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: %s slot %d has dtype %u, expected %u",
+                 step, role, s, slots[s].dtype, dt);
+      return false;
+    }
+    const uint64_t need = (uint64_t)elems * dtype_size(dt);
+    if (slots[s].bytes < need) {
+      err = fail(SHK_HIP_STATUS_RANGE_OUT_OF_BOUNDS,
+                 "step %zu: %s slot %d has %llu bytes, operand needs %llu", step, role, s,
+                 (unsigned long long)slots[s].bytes, (unsigned long long)need);
+      return false;
+    }
+    return true;
+  }
+  bool writable(int32_t s, const char* role) {
+    if (s < 0) return true;
+    if (slots[s].kind == SLOT_INPUT) {
+      err = fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: %s writes read-only input slot %d",
+                 step, role, s);
+      return false;
+    }
+    return true;
+  }
+};
+
+// Extent (in elements) spanned by a row-major matrix view of `rows` x `cols` with leading dim ld.
+int64_t span(int64_t rows, int64_t cols, int64_t ld) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return (rows - 1) * ld + cols;
+}
+
+int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const Step& st,
+                      uint64_t* scratch_doubles) {
+  Validator v{slots, idx};
+  const StepRecord& r = st.rec;
+  const int32_t* s = r.slot;
+  const int64_t* a = r.iarg;
+  auto need = [&](uint64_t d) { *scratch_doubles = std::max<uint64_t>(*scratch_doubles, d); };
+  switch (r.opcode) {
+    case OP_GEMM: {
+      const int64_t M = a[0], N = a[1], K = a[2], lda = a[3], ldb = a[4], ldc = a[5], ldaux = a[6];
+      const int64_t tA = a[7], tB = a[8], act = a[9], mode = a[10];
+      if (M < 0 || N < 0 || K < 0 || (tA != 0 && tA != 1) || (tB != 0 && tB != 1) || act < 0 ||
+          act > 3 || (mode != 0 && mode != 1))
+        return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid GEMM attributes", idx);
+      if (M > INT32_MAX / 2 || N > INT32_MAX / 2)
+        return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: GEMM extent too large", idx);
+      if ((K > 0 && (tA ? lda < std::max<int64_t>(M, 1) : lda < K)) ||
+          (K > 0 && (tB ? ldb < K : ldb < std::max<int64_t>(N, 1))) ||
+          ldc < std::max<int64_t>(N, 1) || (mode == 1 && ldaux < std::max<int64_t>(N, 1)))
+        return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: GEMM leading dimension too small", idx);
+      if (mode == 1 && s[4] < 0)
+        return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: activation gradient needs aux", idx);
+      if (!v.slot_ok(s[0], false, "A") || !v.slot_ok(s[1], false, "B") || !v.slot_ok(s[2], false, "C") ||
+          !v.slot_ok(s[3], true, "bias") || !v.slot_ok(s[4], true, "aux"))
+        return v.err;
+      if (!v.holds(s[0], K == 0 ? 0 : (tA ? span(K, M, lda) : span(M, K, lda)), DT_F32, "A") ||
+          !v.holds(s[1], K == 0 ? 0 : (tB ? span(N, K, ldb) : span(K, N, ldb)), DT_F32, "B") ||
+          !v.holds(s[2], span(M, N, ldc), DT_F32, "C") || !v.holds(s[3], N, DT_F32, "bias") ||
+          !v.holds(s[4], span(M, N, ldaux), DT_F32, "aux") || !v.writable(s[2], "C"))
+        return v.err;
+      return SHK_HIP_STATUS_OK;
+    }
+    case OP_COLSUM: {
+      const int64_t R = a[0], N = a[1], ldx = a[2];
+      if (R < 0 || N < 0 || ldx < std::max<int64_t>(N, 1))
+        return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid COLSUM shape", idx);
+      if (!v.slot_ok(s[0], false, "X") || !v.slot_ok(s[1], false, "out") ||
+          !v.holds(s[0], span(R, N, ldx), DT_F32, "X") || !v.holds(s[1], N, DT_F32, "out") ||
+          !v.writable(s[1], "out"))
+        return v.err;
+      need((uint64_t)shk::colsum_partial_doubles(R, N));
+      return SHK_HIP_STATUS_OK;
+    }
+    case OP_ROW_REDUCE: {
+      const int64_t R = a[0], C = a[1], kind = a[2];
+      if (R < 0 || C < 0 || kind < 0 || kind > 3 || R > INT32_MAX)
+        return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid row reduction", idx);
+      if (!v.slot_ok(s[0], false, "X") || !v.slot_ok(s[1], false, "out") ||
+          !v.holds(s[0], R * C, DT_F32, "X") || !v.holds(s[1], R, DT_F32, "out") ||
+          !v.writable(s[1], "out"))
+        return v.err;
+      return SHK_HIP_STATUS_OK;
+    }
+    case OP_REDUCE_ALL: {
+      const int64_t n = a[0], kind = a[1];
+      if (n < 0 || kind < 0 || kind > 2)
+        return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid reduction", idx);
+      if (!v.slot_ok(s[0], false, "X") || !v.slot_ok(s[1], false, "out") ||
+          !v.holds(s[0], n, DT_F32, "X") || !v.holds(s[1], 1, DT_F32, "out") ||
+          !v.writable(s[1], "out"))
+        return v.err;
+      need((uint64_t)shk::reduce_all_partial_doubles(n));
+      return SHK_HIP_STATUS_OK;
+    }
+    case OP_POINTWISE: {
+      const int64_t R = a[0], C = a[1];
+      if (R < 0 || C < 0) return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid pointwise shape", idx);
+      const size_t n_instr = st.payload.size() / sizeof(shk::PwInstr);
+      if (st.payload.size() % sizeof(shk::PwInstr) != 0 || n_instr == 0 ||
+          n_instr > (size_t)shk::PW_MAX_INSTR)
+        return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: bad pointwise program", idx);
+      for (int k = 0; k < shk::PW_MAX_INPUTS; ++k) {
+        if (!v.slot_ok(s[k], true, "pointwise input")) return v.err;
+        const int64_t mode = a[2 + k];
+        const int64_t ext = mode == 0 ? R * C : mode == 1 ? C : mode == 2 ? R : 1;
+        if (mode < 0 || mode > 3)
+          return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: bad broadcast mode", idx);
+        if (!v.holds(s[k], ext, DT_F32, "pointwise input")) return v.err;
+      }
+      for (int o = 0; o < shk::PW_MAX_OUTPUTS; ++o) {
+        if (!v.slot_ok(s[6 + o], true, "pointwise output") || !v.holds(s[6 + o], R * C, DT_F32, "pointwise output") ||
+            !v.writable(s[6 + o], "pointwise output"))
+          return v.err;
+      }
+      const shk::PwInstr* code = reinterpret_cast<const shk::PwInstr*>(st.payload.data());
+      for (size_t i = 0; i < n_instr; ++i) {
+        const shk::PwInstr& in = code[i];
+        if (in.op > 19 || in.dst >= 8 || in.a >= 8 || in.b >= 8 || in.c >= 8)
+          return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: bad pointwise instruction %zu", idx, i);
+        if (in.op == 0 && (in.a >= shk::PW_MAX_INPUTS || s[in.a] < 0))
+          return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: load of unbound input %u", idx, in.a);
+        if (in.op == 17 && (in.dst >= shk::PW_MAX_OUTPUTS || s[6 + in.dst] < 0))
+          return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: store to unbound output %u", idx, in.dst);
+      }
+      return SHK_HIP_STATUS_OK;
+    }
+    case OP_SOFTMAX: {
+      const int64_t R = a[0], C = a[1];
+      if (R < 0 || C < 0 || R > INT32_MAX)
+        return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid softmax shape", idx);
+      if (!v.slot_ok(s[0], false, "X") || !v.slot_ok(s[1], false, "Y") || !v.slot_ok(s[2], true, "lse") ||
+          !v.holds(s[0], R * C, DT_F32, "X") || !v.holds(s[1], R * C, DT_F32, "Y") ||
+          !v.holds(s[2], R, DT_F32, "lse") || !v.writable(s[1], "Y") || !v.writable(s[2], "lse"))
+        return v.err;
+      return SHK_HIP_STATUS_OK;
+    }
+    case OP_SOFTMAX_BWD: {
+      const int64_t R = a[0], C = a[1];
+      if (R < 0 || C < 0 || R > INT32_MAX)
+        return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid softmax shape", idx);
+      if (!v.slot_ok(s[0], false, "Y") || !v.slot_ok(s[1], false, "G") || !v.slot_ok(s[2], false, "dX") ||
+          !v.slot_ok(s[3], true, "rowscale") || !v.holds(s[0], R * C, DT_F32, "Y") ||
+          !v.holds(s[1], R * C, DT_F32, "G") || !v.holds(s[2], R * C, DT_F32, "dX") ||
+          !v.holds(s[3], R, DT_F32, "rowscale") || !v.writable(s[2], "dX"))
+        return v.err;
+      return SHK_HIP_STATUS_OK;
+    }
+    case OP_LSE_BWD: {
+      const int64_t R = a[0], C = a[1];
+      if (R < 0 || C < 0) return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid LSE shape", idx);
+      if (!v.slot_ok(s[0], false, "X") || !v.slot_ok(s[1], false, "lse") || !v.slot_ok(s[2], true, "g") ||
+          !v.slot_ok(s[3], false, "dX") || !v.holds(s[0], R * C, DT_F32, "X") ||
+          !v.holds(s[1], R, DT_F32, "lse") || !v.holds(s[2], R, DT_F32, "g") ||
+          !v.holds(s[3], R * C, DT_F32, "dX") || !v.writable(s[3], "dX"))
+        return v.err;
+      return SHK_HIP_STATUS_OK;
+    }
+    case OP_MSE: {
+      const int64_t n = a[0];
+      if (n <= 0) return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: MSE needs elements", idx);
+      if (!v.slot_ok(s[0], false, "P") || !v.slot_ok(s[1], false, "T") || !v.slot_ok(s[2], false, "loss") ||
+          !v.slot_ok(s[3], true, "grad") || !v.holds(s[0], n, DT_F32, "P") || !v.holds(s[1], n, DT_F32, "T") ||
+          !v.holds(s[2], 1, DT_F32, "loss") || !v.holds(s[3], n, DT_F32, "grad") ||
+          !v.writable(s[2], "loss") || !v.writable(s[3], "grad"))
+        return v.err;
+      need((uint64_t)shk::mse_partial_doubles(n));
+      return SHK_HIP_STATUS_OK;
+    }
+    case OP_CE_INDEX: {
+      const int64_t R = a[0], C = a[1], is64 = a[2];
+      if (R < 0 || C <= 0 || (is64 != 0 && is64 != 1))
+        return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid cross-entropy shape", idx);
+      if (!v.slot_ok(s[0], false, "logits") || !v.slot_ok(s[1], false, "target") ||
+          !v.slot_ok(s[2], false, "loss") || !v.slot_ok(s[3], true, "grad") ||
+          !v.holds(s[0], R * C, DT_F32, "logits") || !v.holds(s[1], R, is64 ? DT_I64 : DT_I32, "target") ||
+          !v.holds(s[2], 1, DT_F32, "loss") || !v.holds(s[3], R * C, DT_F32, "grad") ||
+          !v.writable(s[2], "loss") || !v.writable(s[3], "grad"))
+        return v.err;
+      need((uint64_t)shk::index_ce_partial_doubles(R));
+      return SHK_HIP_STATUS_OK;
+    }
+    case OP_OPTIMIZER: {
+      const int64_t kind = a[0], phase = a[1];
+      if (kind < 0 || kind > 2 || (phase != 0 && phase != 1))
+        return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: invalid optimizer", idx);
+      if (!v.slot_ok(s[0], false, "step counter") || !v.holds(s[0], 1, DT_I64, "step counter"))
+        return v.err;
+      const size_t n = st.payload.size() / sizeof(OptEntry);
+      if (st.payload.size() % sizeof(OptEntry) != 0 || n == 0 || n > (size_t)shk::OPT_MAX_TENSORS)
+        return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: bad optimizer tensor table", idx);
+      const OptEntry* e = reinterpret_cast<const OptEntry*>(st.payload.data());
+      for (size_t i = 0; i < n; ++i) {
+        const bool adam = kind != 0;
+        if (!v.slot_ok(e[i].p, false, "param") || !v.slot_ok(e[i].g, false, "grad") ||
+            !v.slot_ok(e[i].m, !adam, "momentum") || !v.slot_ok(e[i].v, !adam, "second moment") ||
+            !v.holds(e[i].p, e[i].n, DT_F32, "param") || !v.holds(e[i].g, e[i].n, DT_F32, "grad") ||
+            !v.holds(e[i].m, e[i].n, DT_F32, "momentum") || !v.holds(e[i].v, e[i].n, DT_F32, "second moment") ||
+            !v.writable(e[i].p, "param") || !v.writable(e[i].m, "momentum") || !v.writable(e[i].v, "second moment"))
+          return v.err;
+      }
+      return SHK_HIP_STATUS_OK;
+    }
+    case OP_STEP_COMMIT:
+      if (!v.slot_ok(s[0], false, "step counter") || !v.holds(s[0], 1, DT_I64, "step counter") ||
+          !v.writable(s[0], "step counter"))
+        return v.err;
+      return SHK_HIP_STATUS_OK;
+    case OP_FILL:
+      if (a[0] < 0) return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid fill", idx);
+      if (!v.slot_ok(s[0], false, "X") || !v.holds(s[0], a[0], DT_F32, "X") || !v.writable(s[0], "X"))
+        return v.err;
+      return SHK_HIP_STATUS_OK;
+    case OP_COPY:
+      if (a[0] < 0) return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid copy", idx);
+      if (!v.slot_ok(s[0], false, "src") || !v.slot_ok(s[1], false, "dst") ||
+          !v.holds(s[0], a[0], DT_F32, "src") || !v.holds(s[1], a[0], DT_F32, "dst") ||
+          !v.writable(s[1], "dst"))
+        return v.err;
+      return SHK_HIP_STATUS_OK;
+    default:
+      return fail(SHK_HIP_STATUS_UNSUPPORTED_OPERATION, "step %zu: unknown opcode %u", idx, r.opcode);
+  }
+}
+
+// ---- run-time dispatch ----
+struct Bound {
+  std::vector<void*> ptr;  // device pointer per slot
+  template <typename T>
+  T* get(int32_t s) const { return s < 0 ? nullptr : static_cast<T*>(ptr[s]); }
+};
+
+hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipStream_t stream) {
+  const StepRecord& r = st.rec;
+  const int32_t* s = r.slot;
+  const int64_t* a = r.iarg;
+  switch (r.opcode) {
+    case OP_GEMM: {
+      shk::GemmParams p{};
+      p.A = b.get<const float>(s[0]);
+      p.B = b.get<const float>(s[1]);
+      p.C = b.get<float>(s[2]);
+      p.bias = b.get<const float>(s[3]);
+      p.aux = b.get<const float>(s[4]);
+      p.M = a[0]; p.N = a[1]; p.K = a[2];
+      p.lda = a[3]; p.ldb = a[4]; p.ldc = a[5]; p.ldaux = a[6];
+      p.transA = (int)a[7]; p.transB = (int)a[8];
+      p.act = (int)a[9]; p.mode = (int)a[10]; p.accumulate = (int)a[11];
+      return shk::launch_gemm(p, stream);
+    }
+    case OP_COLSUM:
+      return shk::launch_colsum(b.get<const float>(s[0]), b.get<float>(s[1]), a[0], a[1], a[2],
+                                a[4] ? (double)a[0] : 1.0, (int)a[3], pr.scratch, stream);
+    case OP_ROW_REDUCE:
+      return shk::launch_row_reduce(b.get<const float>(s[0]), b.get<float>(s[1]), a[0], a[1], (int)a[2], stream);
+    case OP_REDUCE_ALL:
+      return shk::launch_reduce_all(b.get<const float>(s[0]), b.get<float>(s[1]), a[0], (int)a[1],
+                                    pr.scratch, stream);
+    case OP_POINTWISE: {
+      shk::PwParams p{};
+      for (int k = 0; k < shk::PW_MAX_INPUTS; ++k) {
+        p.in[k] = b.get<const float>(s[k]);
+        p.in_mode[k] = a[2 + k];
+      }
+      for (int o = 0; o < shk::PW_MAX_OUTPUTS; ++o) p.out[o] = b.get<float>(s[6 + o]);
+      p.R = a[0]; p.C = a[1];
+      p.n_instr = (int)(st.payload.size() / sizeof(shk::PwInstr));
+      memcpy(p.code, st.payload.data(), st.payload.size());
+      return shk::launch_pointwise(p, stream);
+    }
+    case OP_SOFTMAX:
+      return shk::launch_softmax_fwd(b.get<const float>(s[0]), b.get<float>(s[1]), b.get<float>(s[2]),
+                                     a[0], a[1], (int)a[2], stream);
+    case OP_SOFTMAX_BWD:
+      return shk::launch_softmax_bwd(b.get<const float>(s[0]), b.get<const float>(s[1]), b.get<float>(s[2]),
+                                     a[0], a[1], b.get<const float>(s[3]), r.farg[0], stream);
+    case OP_LSE_BWD:
+      return shk::launch_lse_bwd(b.get<const float>(s[0]), b.get<const float>(s[1]), b.get<const float>(s[2]),
+                                 r.farg[0], b.get<float>(s[3]), a[0], a[1], stream);
+    case OP_MSE:
+      return shk::launch_mse(b.get<const float>(s[0]), b.get<const float>(s[1]), b.get<float>(s[2]),
+                             b.get<float>(s[3]), a[0], r.farg[0], pr.scratch, stream);
+    case OP_CE_INDEX:
+      return shk::launch_index_ce(b.get<const float>(s[0]), b.get<const void>(s[1]), (int)a[2],
+                                  b.get<float>(s[2]), b.get<float>(s[3]), a[0], a[1], (int)a[3], a[4],
+                                  r.farg[0], pr.scratch, pr.status, stream);
+    case OP_OPTIMIZER: {
+      shk::OptParams p{};
+      const OptEntry* e = reinterpret_cast<const OptEntry*>(st.payload.data());
+      p.count = (int)(st.payload.size() / sizeof(OptEntry));
+      for (int i = 0; i < p.count; ++i) {
+        p.t[i].p = b.get<float>(e[i].p);
+        p.t[i].g = b.get<const float>(e[i].g);
+        p.t[i].m = b.get<float>(e[i].m);
+        p.t[i].v = b.get<float>(e[i].v);
+        p.t[i].n = e[i].n;
+      }
+      p.kind = (int)a[0]; p.phase = (int)a[1]; p.nesterov = (int)a[2]; p.has_momentum_slot = (int)a[3];
+      p.lr = r.farg[0]; p.momentum = r.farg[1]; p.dampening = r.farg[2]; p.weight_decay = r.farg[3];
+      p.beta1 = r.farg[4]; p.beta2 = r.farg[5]; p.eps = r.farg[6];
+      p.completed_steps = b.get<const int64_t>(s[0]);
+      p.status = pr.status;
+      return shk::launch_optimizer(p, stream);
+    }
+    case OP_STEP_COMMIT:
+      return shk::launch_step_commit(b.get<int64_t>(s[0]), pr.status, stream);
+    case OP_FILL:
+      return shk::launch_fill(b.get<float>(s[0]), a[0], r.farg[0], stream);
+    case OP_COPY:
+      return shk::launch_copy(b.get<const float>(s[0]), b.get<float>(s[1]), a[0], stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+void destroy_program(Program* p) {
+  if (p == nullptr) return;
+  for (hipEvent_t e : p->events) (void)hipEventDestroy(e);
+  if (p->arena != nullptr) (void)hipFree(p->arena);
+  p->magic = 0;
+  delete p;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t shk_hip_abi_version(void) { return SHK_HIP_ABI_VERSION; }
+
+int32_t shk_hip_last_error(char* destination, uint64_t capacity) {
+  if (destination == nullptr || capacity == 0) return SHK_HIP_STATUS_INVALID_ARGUMENT;
+  const size_t n = std::min<size_t>(capacity - 1, g_last_error.size());
+  memcpy(destination, g_last_error.data(), n);
+  destination[n] = '\0';
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_context_create(int32_t device_ordinal, void** out_context) {
+  if (out_context == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "out_context is null");
+  *out_context = nullptr;
+  try {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+      return fail(SHK_HIP_STATUS_NO_DEVICE, "no HIP device is available");
+    if (device_ordinal < 0 || device_ordinal >= count)
+      return fail(SHK_HIP_STATUS_NO_DEVICE, "device ordinal %d outside [0,%d)", device_ordinal, count);
+    HIP_TRY(hipSetDevice(device_ordinal));
+    Context* c = new Context();
+    c->device = device_ordinal;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+      delete c;
+      return fail(SHK_HIP_STATUS_NO_COMMAND_QUEUE, "hipStreamCreateWithFlags failed");
+    }
+    if (hipHostMalloc((void**)&c->host_status, 16, hipHostMallocDefault) != hipSuccess) {
+      (void)hipStreamDestroy(c->stream);
+      delete c;
+      return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "pinned status allocation failed");
+    }
+    *out_context = c;
+    return SHK_HIP_STATUS_OK;
+  } catch (const std::bad_alloc&) {
+    return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "host allocation failed");
+  } catch (...) {
+    return fail(SHK_HIP_STATUS_INTERNAL_ERROR, "unexpected exception");
+  }
+}
+
+int32_t shk_hip_context_release(void* context) {
+  Context* c = checked<Context, kContextMagic>(context);
+  if (c == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a context handle");
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  (void)hipStreamDestroy(c->stream);
+  (void)hipHostFree(c->host_status);
+  c->magic = 0;
+  delete c;
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_device_info(void* context, int32_t* out_compute_units, int32_t* out_clock_khz,
+                            uint64_t* out_memory_bytes, char* out_name, uint64_t name_capacity) {
+  Context* c = checked<Context, kContextMagic>(context);
+  if (c == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a context handle");
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, c->device));
+  if (out_compute_units) *out_compute_units = prop.multiProcessorCount;
+  if (out_clock_khz) *out_clock_khz = prop.clockRate;
+  if (out_memory_bytes) *out_memory_bytes = prop.totalGlobalMem;
+  if (out_name && name_capacity > 0) {
+    const size_t n = std::min<size_t>(name_capacity - 1, strlen(prop.gcnArchName));
+    memcpy(out_name, prop.gcnArchName, n);
+    out_name[n] = '\0';
+  }
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_buffer_create(void* context, uint64_t byte_size, void** out_buffer) {
+  if (out_buffer == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "out_buffer is null");
+  *out_buffer = nullptr;
+  Context* c = checked<Context, kContextMagic>(context);
+  if (c == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a context handle");
+  try {
+    HIP_TRY(hipSetDevice(c->device));
+    void* p = nullptr;
+    if (hipMalloc(&p, std::max<uint64_t>(byte_size, 256)) != hipSuccess)
+      return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "hipMalloc of %llu bytes failed",
+                  (unsigned long long)byte_size);
+    Buffer* b = new Buffer();
+    b->ctx = c;
+    b->ptr = p;
+    b->bytes = byte_size;
+    *out_buffer = b;
+    return SHK_HIP_STATUS_OK;
+  } catch (...) {
+    return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "host allocation failed");
+  }
+}
+
+int32_t shk_hip_buffer_wrap(void* context, void* device_pointer, uint64_t byte_size, void** out_buffer) {
+  if (out_buffer == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "out_buffer is null");
+  *out_buffer = nullptr;
+  Context* c = checked<Context, kContextMagic>(context);
+  if (c == nullptr || (device_pointer == nullptr && byte_size != 0))
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid wrap arguments");
+  try {
+    Buffer* b = new Buffer();
+    b->ctx = c;
+    b->ptr = device_pointer;
+    b->bytes = byte_size;
+    b->owned = false;
+    *out_buffer = b;
+    return SHK_HIP_STATUS_OK;
+  } catch (...) {
+    return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "host allocation failed");
+  }
+}
+
+int32_t shk_hip_buffer_release(void* buffer) {
+  Buffer* b = checked<Buffer, kBufferMagic>(buffer);
+  if (b == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a buffer handle");
+  if (b->owned && b->ptr != nullptr) {
+    (void)hipSetDevice(b->ctx->device);
+    (void)hipFree(b->ptr);
+  }
+  b->magic = 0;
+  delete b;
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_buffer_upload(void* buffer, uint64_t offset, const void* source, uint64_t byte_count) {
+  Buffer* b = checked<Buffer, kBufferMagic>(buffer);
+  if (b == nullptr || (source == nullptr && byte_count != 0))
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid upload arguments");
+  if (offset > b->bytes || byte_count > b->bytes - offset)
+    return fail(SHK_HIP_STATUS_RANGE_OUT_OF_BOUNDS, "upload range outside the buffer");
+  if (byte_count == 0) return SHK_HIP_STATUS_OK;
+  std::lock_guard<std::mutex> lock(b->ctx->mutex);
+  HIP_TRY(hipSetDevice(b->ctx->device));
+  if (hipMemcpyAsync(static_cast<char*>(b->ptr) + offset, source, byte_count, hipMemcpyHostToDevice,
+                     b->ctx->stream) != hipSuccess ||
+      hipStreamSynchronize(b->ctx->stream) != hipSuccess)
+    return fail(SHK_HIP_STATUS_COPY_FAILED, "host-to-device copy failed");
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_buffer_download(void* buffer, uint64_t offset, void* destination, uint64_t byte_count) {
+  Buffer* b = checked<Buffer, kBufferMagic>(buffer);
+  if (b == nullptr || (destination == nullptr && byte_count != 0))
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid download arguments");
+  if (offset > b->bytes || byte_count > b->bytes - offset)
+    return fail(SHK_HIP_STATUS_RANGE_OUT_OF_BOUNDS, "download range outside the buffer");
+  if (byte_count == 0) return SHK_HIP_STATUS_OK;
+  std::lock_guard<std::mutex> lock(b->ctx->mutex);
+  HIP_TRY(hipSetDevice(b->ctx->device));
+  if (hipMemcpyAsync(destination, static_cast<const char*>(b->ptr) + offset, byte_count,
+                     hipMemcpyDeviceToHost, b->ctx->stream) != hipSuccess ||
+      hipStreamSynchronize(b->ctx->stream) != hipSuccess)
+    return fail(SHK_HIP_STATUS_COPY_FAILED, "device-to-host copy failed");
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_buffer_device_pointer(void* buffer, void** out_pointer) {
+  if (out_pointer == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "out_pointer is null");
+  *out_pointer = nullptr;
+  Buffer* b = checked<Buffer, kBufferMagic>(buffer);
+  if (b == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a buffer handle");
+  *out_pointer = b->ptr;
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_bytes, void** out_program) {
+  if (out_program == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "out_program is null");
+  *out_program = nullptr;
+  Context* c = checked<Context, kContextMagic>(context);
+  if (c == nullptr || image == nullptr)
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid program arguments");
+  Program* pr = nullptr;
+  try {
+    const uint8_t* p = static_cast<const uint8_t*>(image);
+    const uint8_t* end = p + image_bytes;
+    if (image_bytes < sizeof(ImageHeader))
+      return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image shorter than its header");
+    ImageHeader h;
+    memcpy(&h, p, sizeof h);
+    p += sizeof h;
+    if (h.magic != kImageMagic || h.version != kImageVersion)
+      return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image magic/version mismatch");
+    if (h.n_slots > 1u << 20 || h.n_steps > 1u << 20 ||
+        (uint64_t)(end - p) < (uint64_t)h.n_slots * sizeof(SlotRecord))
+      return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image slot table truncated");
+    pr = new Program();
+    pr->ctx = c;
+    pr->slots.resize(h.n_slots);
+    memcpy(pr->slots.data(), p, h.n_slots * sizeof(SlotRecord));
+    p += h.n_slots * sizeof(SlotRecord);
+    std::vector<int> in_seen, out_seen;
+    for (uint32_t i = 0; i < h.n_slots; ++i) {
+      const SlotRecord& s = pr->slots[i];
+      if (dtype_size(s.dtype) == 0 || s.kind > SLOT_INOUT) {
+        destroy_program(pr);
+        return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "slot %u has an invalid dtype or kind", i);
+      }
+      if (s.kind == SLOT_INPUT || s.kind == SLOT_INOUT) {
+        if (s.ext_index >= in_seen.size()) in_seen.resize(s.ext_index + 1, 0);
+        in_seen[s.ext_index]++;
+      } else if (s.kind == SLOT_OUTPUT) {
+        if (s.ext_index >= out_seen.size()) out_seen.resize(s.ext_index + 1, 0);
+        out_seen[s.ext_index]++;
+      }
+    }
+    for (size_t i = 0; i < in_seen.size(); ++i)
+      if (in_seen[i] != 1) {
+        destroy_program(pr);
+        return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "input index %zu bound %d times", i, in_seen[i]);
+      }
+    for (size_t i = 0; i < out_seen.size(); ++i)
+      if (out_seen[i] != 1) {
+        destroy_program(pr);
+        return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "output index %zu bound %d times", i, out_seen[i]);
+      }
+    pr->n_inputs = (uint32_t)in_seen.size();
+    pr->n_outputs = (uint32_t)out_seen.size();
+
+    uint64_t scratch_doubles = 0;
+    pr->steps.resize(h.n_steps);
+    for (uint32_t i = 0; i < h.n_steps; ++i) {
+      if ((uint64_t)(end - p) < sizeof(StepRecord)) {
+        destroy_program(pr);
+        return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image step %u truncated", i);
+      }
+      Step& st = pr->steps[i];
+      memcpy(&st.rec, p, sizeof(StepRecord));
+      p += sizeof(StepRecord);
+      const uint64_t padded = (st.rec.payload_bytes + 7u) & ~7ull;
+      if (st.rec.payload_bytes > 65536 || (uint64_t)(end - p) < padded) {
+        destroy_program(pr);
+        return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image step %u payload truncated", i);
+      }
+      st.payload.assign(p, p + st.rec.payload_bytes);
+      p += padded;
+      const int32_t v = validate_step(pr->slots, i, st, &scratch_doubles);
+      if (v != SHK_HIP_STATUS_OK) {
+        destroy_program(pr);
+        return v;
+      }
+    }
+    if (p != end) {
+      destroy_program(pr);
+      return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image has trailing bytes");
+    }
+
+    // Arena: status word, reduction scratch, then 256-byte aligned internal slots.
+    uint64_t off = 256;
+    const uint64_t scratch_off = off;
+    off += ((scratch_doubles * 8 + 255) / 256) * 256;
+    pr->internal_offset.assign(h.n_slots, 0);
+    for (uint32_t i = 0; i < h.n_slots; ++i) {
+      if (pr->slots[i].kind != SLOT_INTERNAL) continue;
+      pr->internal_offset[i] = off;
+      off += ((pr->slots[i].bytes + 255) / 256) * 256;
+    }
+    pr->arena_bytes = off;
+    if (hipSetDevice(c->device) != hipSuccess || hipMalloc(&pr->arena, off) != hipSuccess) {
+      pr->arena = nullptr;
+      destroy_program(pr);
+      return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "program arena of %llu bytes failed",
+                  (unsigned long long)off);
+    }
+    // Internal slots start zeroed (optimizer slots, accumulators).
+    if (hipMemset(pr->arena, 0, off) != hipSuccess) {
+      destroy_program(pr);
+      return fail(SHK_HIP_STATUS_DEVICE_ERROR, "arena initialisation failed");
+    }
+    pr->status = static_cast<uint32_t*>(pr->arena);
+    pr->scratch = reinterpret_cast<double*>(static_cast<char*>(pr->arena) + scratch_off);
+    pr->step_ms.assign(h.n_steps, 0.0);
+    *out_program = pr;
+    return SHK_HIP_STATUS_OK;
+  } catch (const std::bad_alloc&) {
+    destroy_program(pr);
+    return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "host allocation failed");
+  } catch (...) {
+    destroy_program(pr);
+    return fail(SHK_HIP_STATUS_INTERNAL_ERROR, "unexpected exception");
+  }
+}
+
+int32_t shk_hip_program_release(void* program) {
+  Program* pr = checked<Program, kProgramMagic>(program);
+  if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
+  {
+    std::lock_guard<std::mutex> lock(pr->ctx->mutex);
+    (void)hipSetDevice(pr->ctx->device);
+    (void)hipStreamSynchronize(pr->ctx->stream);
+  }
+  destroy_program(pr);
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_program_arena_bytes(void* program, uint64_t* out_bytes) {
+  Program* pr = checked<Program, kProgramMagic>(program);
+  if (pr == nullptr || out_bytes == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid arguments");
+  *out_bytes = pr->arena_bytes;
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_program_step_count(void* program, uint32_t* out_steps) {
+  Program* pr = checked<Program, kProgramMagic>(program);
+  if (pr == nullptr || out_steps == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid arguments");
+  *out_steps = (uint32_t)pr->steps.size();
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_program_set_profiling(void* program, int32_t enabled) {
+  Program* pr = checked<Program, kProgramMagic>(program);
+  if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
+  std::lock_guard<std::mutex> lock(pr->run_mutex);
+  if (enabled && pr->events.empty()) {
+    (void)hipSetDevice(pr->ctx->device);
+    pr->events.resize(pr->steps.size() + 1, nullptr);
+    for (auto& e : pr->events) HIP_TRY(hipEventCreate(&e));
+  }
+  pr->profiling = enabled != 0;
+  pr->profiled_runs = 0;
+  std::fill(pr->step_ms.begin(), pr->step_ms.end(), 0.0);
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_program_step_times(void* program, double* out_milliseconds, uint32_t capacity, uint64_t* out_runs) {
+  Program* pr = checked<Program, kProgramMagic>(program);
+  if (pr == nullptr || (out_milliseconds == nullptr && capacity != 0))
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid arguments");
+  std::lock_guard<std::mutex> lock(pr->run_mutex);
+  for (uint32_t i = 0; i < capacity && i < pr->step_ms.size(); ++i) out_milliseconds[i] = pr->step_ms[i];
+  if (out_runs) *out_runs = pr->profiled_runs;
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_program_run(void* program, uint32_t input_count, void* const* inputs,
+                            uint32_t output_count, void* const* outputs) {
+  Program* pr = checked<Program, kProgramMagic>(program);
+  if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
+  if (input_count != pr->n_inputs || output_count != pr->n_outputs)
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "program expects %u inputs and %u outputs, got %u and %u",
+                pr->n_inputs, pr->n_outputs, input_count, output_count);
+  if ((input_count && inputs == nullptr) || (output_count && outputs == nullptr))
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "null binding array");
+  try {
+    std::vector<Buffer*> in(input_count), out(output_count);
+    for (uint32_t i = 0; i < input_count; ++i) {
+      in[i] = checked<Buffer, kBufferMagic>(inputs[i]);
+      if (in[i] == nullptr || in[i]->ctx != pr->ctx)
+        return fail(SHK_HIP_STATUS_INCOMPATIBLE_RESOURCE, "input %u is not a buffer of this context", i);
+    }
+    for (uint32_t i = 0; i < output_count; ++i) {
+      out[i] = checked<Buffer, kBufferMagic>(outputs[i]);
+      if (out[i] == nullptr || out[i]->ctx != pr->ctx)
+        return fail(SHK_HIP_STATUS_INCOMPATIBLE_RESOURCE, "output %u is not a buffer of this context", i);
+    }
+    Bound b;
+    b.ptr.assign(pr->slots.size(), nullptr);
+    std::vector<std::pair<uintptr_t, uintptr_t>> written;  // [begin,end) of outputs and in-place inputs
+    std::vector<std::pair<uintptr_t, uintptr_t>> all;
+    for (size_t i = 0; i < pr->slots.size(); ++i) {
+      const SlotRecord& s = pr->slots[i];
+      if (s.kind == SLOT_INTERNAL) {
+        b.ptr[i] = static_cast<char*>(pr->arena) + pr->internal_offset[i];
+        continue;
+      }
+      Buffer* buf = s.kind == SLOT_OUTPUT ? out[s.ext_index] : in[s.ext_index];
+      if (buf->bytes < s.bytes)
+        return fail(SHK_HIP_STATUS_INCOMPATIBLE_RESOURCE, "slot %zu needs %llu bytes, bound buffer has %llu", i,
+                    (unsigned long long)s.bytes, (unsigned long long)buf->bytes);
+      b.ptr[i] = buf->ptr;
+      const uintptr_t lo = reinterpret_cast<uintptr_t>(buf->ptr), hi = lo + std::max<uint64_t>(s.bytes, 1);
+      if (s.kind != SLOT_INPUT) written.push_back({lo, hi});
+      all.push_back({lo, hi});
+    }
+    // A written buffer may not overlap any other bound buffer (Metal: synaptik_metal_foundation.m:10012-10020).
+    for (const auto& w : written) {
+      int overlaps = 0;
+      for (const auto& o : all)
+        if (o.first < w.second && w.first < o.second) ++overlaps;
+      if (overlaps > 1)
+        return fail(SHK_HIP_STATUS_INCOMPATIBLE_RESOURCE, "an output or in-place input aliases another binding");
+    }
+
+    std::lock_guard<std::mutex> run_lock(pr->run_mutex);
+    std::lock_guard<std::mutex> ctx_lock(pr->ctx->mutex);
+    HIP_TRY(hipSetDevice(pr->ctx->device));
+    hipStream_t stream = pr->ctx->stream;
+    HIP_TRY(shk::launch_fill_u32(pr->status, 4, 0u, stream));
+    for (size_t i = 0; i < pr->steps.size(); ++i) {
+      if (pr->profiling) HIP_TRY(hipEventRecord(pr->events[i], stream));
+      const hipError_t e = enqueue_step(*pr, pr->steps[i], b, stream);
+      if (e != hipSuccess) {
+        (void)hipStreamSynchronize(stream);
+        return fail(SHK_HIP_STATUS_EXECUTION_FAILED, "step %zu (opcode %u) launch failed: %s", i,
+                    pr->steps[i].rec.opcode, hipGetErrorName(e));
+      }
+    }
+    if (pr->profiling) HIP_TRY(hipEventRecord(pr->events[pr->steps.size()], stream));
+    HIP_TRY(hipMemcpyAsync(pr->ctx->host_status, pr->status, 4, hipMemcpyDeviceToHost, stream));
+    const hipError_t se = hipStreamSynchronize(stream);
+    if (se != hipSuccess)
+      return fail(SHK_HIP_STATUS_EXECUTION_FAILED, "program execution failed: %s", hipGetErrorName(se));
+    if (pr->profiling) {
+      for (size_t i = 0; i < pr->steps.size(); ++i) {
+        float ms = 0.f;
+        HIP_TRY(hipEventElapsedTime(&ms, pr->events[i], pr->events[i + 1]));
+        pr->step_ms[i] += ms;
+      }
+      pr->profiled_runs++;
+    }
+    const uint32_t st = *pr->ctx->host_status;
+    if (st & shk::DEV_INDEX_OUT_OF_BOUNDS)
+      return fail(SHK_HIP_STATUS_INDEX_OUT_OF_BOUNDS, "index target out of bounds");
+    if (st & shk::DEV_NOT_POSITIVE)
+      return fail(SHK_HIP_STATUS_ARITHMETIC, "adaptive bias correction or denominator is not positive");
+    if (st & shk::DEV_NON_FINITE)
+      return fail(SHK_HIP_STATUS_ARITHMETIC, "optimizer intermediate or candidate is not finite");
+    return SHK_HIP_STATUS_OK;
+  } catch (const std::bad_alloc&) {
+    return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "host allocation failed");
+  } catch (...) {
+    return fail(SHK_HIP_STATUS_INTERNAL_ERROR, "unexpected exception");
+  }
+}
+
+}  // extern "C"

@@ -1,0 +1,450 @@
+// Row softmax / log-softmax / log-sum-exp and the MSE and index categorical cross-entropy losses.
+//
+// Softmax follows CpuSoftmaxReferenceKernel.evaluateFloat (reference/CpuSoftmaxReferenceKernel.java:104-146):
+//   maximum by Math.max; a +inf maximum maps +inf entries to NaN and the rest to 0 (softmax) or
+//   -inf (log-softmax); a row containing -inf (and no NaN) is evaluated unshifted (shift 0);
+//   addends are (float)exp((double)(x - shift)); the result is (float)exp(shift)/sum or
+//   shift - (float)log(sum). The reference sums addends with Kahan compensation in binary32; the
+//   GPU sums the same binary32 addends in binary64 through a fixed tree and rounds once, so both
+//   sums are within a few binary32 ulps of the exact sum (reduction-order difference).
+// One 256-thread workgroup owns one row; rows up to 4096 wide are held in registers
+// (one HBM read and one write per element), wider rows are streamed three times.
+#include "common.h"
+#include "kernels.h"
+#include <algorithm>
+
+namespace shk {
+namespace {
+
+constexpr int SM_NT = 256;
+
+__device__ __forceinline__ int block_or(int v, int* lds) {
+  v = wave_or(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int r = 0;
+#pragma unroll
+  for (int i = 0; i < SM_NT / 64; ++i) r |= lds[i];
+  return r;
+}
+
+struct RowStats {
+  float shift;
+  float sum;
+  bool pos_inf;
+};
+
+__device__ __forceinline__ float shifted_exp(float x, float shift) {
+  return (float)exp((double)(x - shift));
+}
+
+// V float4 per thread in registers (C <= V * 4 * SM_NT, C % 4 == 0).
+template <int V>
+__global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restrict__ x,
+                                                          float* __restrict__ y, float* lse,
+                                                          int64_t C, int log_softmax) {
+  __shared__ double dl[SM_NT / 64];
+  __shared__ float fl[SM_NT / 64];
+  __shared__ int il[SM_NT / 64];
+  const int64_t r = blockIdx.x;
+  const float4* xr = reinterpret_cast<const float4*>(x + r * C);
+  float4* yr = reinterpret_cast<float4*>(y + r * C);
+  const int C4 = (int)(C / 4);
+  float4 v[V];
+  float m = -INFINITY;
+  int neg_inf = 0;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = threadIdx.x + i * SM_NT;
+    if (c < C4) {
+      v[i] = xr[c];
+      m = java_max(java_max(m, v[i].x), java_max(v[i].y, java_max(v[i].z, v[i].w)));
+      neg_inf |= (v[i].x == -INFINITY) | (v[i].y == -INFINITY) | (v[i].z == -INFINITY) |
+                 (v[i].w == -INFINITY);
+    }
+  }
+  m = block_max<SM_NT>(m, fl);
+  neg_inf = block_or(neg_inf, il);
+  if (m == INFINITY) {
+    const float other = log_softmax ? -INFINITY : 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int c = threadIdx.x + i * SM_NT;
+      if (c < C4) {
+        float4 o;
+        o.x = v[i].x == INFINITY ? NAN : other;
+        o.y = v[i].y == INFINITY ? NAN : other;
+        o.z = v[i].z == INFINITY ? NAN : other;
+        o.w = v[i].w == INFINITY ? NAN : other;
+        yr[c] = o;
+      }
+    }
+    if (lse != nullptr && threadIdx.x == 0) lse[r] = INFINITY;
+    return;
+  }
+  const float shift = (neg_inf && m == m) ? 0.0f : m;
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = threadIdx.x + i * SM_NT;
+    if (c < C4) {
+      s += (double)shifted_exp(v[i].x, shift);
+      s += (double)shifted_exp(v[i].y, shift);
+      s += (double)shifted_exp(v[i].z, shift);
+      s += (double)shifted_exp(v[i].w, shift);
+    }
+  }
+  const float sum = (float)block_sum<SM_NT>(s, dl);
+  const float logsum = (float)log((double)sum);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = threadIdx.x + i * SM_NT;
+    if (c < C4) {
+      float4 o;
+      if (log_softmax) {
+        o.x = (v[i].x - shift) - logsum;
+        o.y = (v[i].y - shift) - logsum;
+        o.z = (v[i].z - shift) - logsum;
+        o.w = (v[i].w - shift) - logsum;
+      } else {
+        o.x = shifted_exp(v[i].x, shift) / sum;
+        o.y = shifted_exp(v[i].y, shift) / sum;
+        o.z = shifted_exp(v[i].z, shift) / sum;
+        o.w = shifted_exp(v[i].w, shift) / sum;
+      }
+      yr[c] = o;
+    }
+  }
+  if (lse != nullptr && threadIdx.x == 0) lse[r] = shift + logsum;
+}
+
+// Any width: three streaming passes over the row.
+__global__ void __launch_bounds__(SM_NT) softmax_fwd_stream(const float* __restrict__ x,
+                                                            float* __restrict__ y, float* lse,
+                                                            int64_t C, int log_softmax) {
+  __shared__ double dl[SM_NT / 64];
+  __shared__ float fl[SM_NT / 64];
+  __shared__ int il[SM_NT / 64];
+  const int64_t r = blockIdx.x;
+  const float* xr = x + r * C;
+  float* yr = y + r * C;
+  float m = -INFINITY;
+  int neg_inf = 0;
+  for (int64_t c = threadIdx.x; c < C; c += SM_NT) {
+    const float t = xr[c];
+    m = java_max(m, t);
+    neg_inf |= t == -INFINITY;
+  }
+  m = block_max<SM_NT>(m, fl);
+  neg_inf = block_or(neg_inf, il);
+  if (m == INFINITY) {
+    const float other = log_softmax ? -INFINITY : 0.0f;
+    for (int64_t c = threadIdx.x; c < C; c += SM_NT) yr[c] = xr[c] == INFINITY ? NAN : other;
+    if (lse != nullptr && threadIdx.x == 0) lse[r] = INFINITY;
+    return;
+  }
+  const float shift = (neg_inf && m == m) ? 0.0f : m;
+  double s = 0.0;
+  for (int64_t c = threadIdx.x; c < C; c += SM_NT) s += (double)shifted_exp(xr[c], shift);
+  const float sum = (float)block_sum<SM_NT>(s, dl);
+  const float logsum = (float)log((double)sum);
+  for (int64_t c = threadIdx.x; c < C; c += SM_NT)
+    yr[c] = log_softmax ? (xr[c] - shift) - logsum : shifted_exp(xr[c], shift) / sum;
+  if (lse != nullptr && threadIdx.x == 0) lse[r] = C == 0 ? -INFINITY : shift + logsum;
+}
+
+// dX = y (.) (g - s) [+ k_r * y], s = sum(g (.) y)  (ReductionGradientRules.java:84-90).
+template <int V>
+__global__ void __launch_bounds__(SM_NT) softmax_bwd_regs(const float* __restrict__ y,
+                                                          const float* __restrict__ g,
+                                                          float* __restrict__ dx, int64_t C,
+                                                          const float* rowscale, float rsc) {
+  __shared__ double dl[SM_NT / 64];
+  const int64_t r = blockIdx.x;
+  const float4* yr = reinterpret_cast<const float4*>(y + r * C);
+  const float4* gr = reinterpret_cast<const float4*>(g + r * C);
+  float4* dr = reinterpret_cast<float4*>(dx + r * C);
+  const int C4 = (int)(C / 4);
+  float4 yv[V], gv[V];
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = threadIdx.x + i * SM_NT;
+    if (c < C4) {
+      yv[i] = yr[c];
+      gv[i] = gr[c];
+      s += (double)(gv[i].x * yv[i].x);
+      s += (double)(gv[i].y * yv[i].y);
+      s += (double)(gv[i].z * yv[i].z);
+      s += (double)(gv[i].w * yv[i].w);
+    }
+  }
+  const float sf = (float)block_sum<SM_NT>(s, dl);
+  const bool scaled = rowscale != nullptr || rsc != 0.0f;
+  const float k = rowscale != nullptr ? rowscale[r] : rsc;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = threadIdx.x + i * SM_NT;
+    if (c < C4) {
+      float4 o;
+      o.x = yv[i].x * (gv[i].x - sf);
+      o.y = yv[i].y * (gv[i].y - sf);
+      o.z = yv[i].z * (gv[i].z - sf);
+      o.w = yv[i].w * (gv[i].w - sf);
+      if (scaled) {
+        o.x = o.x + k * yv[i].x;
+        o.y = o.y + k * yv[i].y;
+        o.z = o.z + k * yv[i].z;
+        o.w = o.w + k * yv[i].w;
+      }
+      dr[c] = o;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(SM_NT) softmax_bwd_stream(const float* __restrict__ y,
+                                                            const float* __restrict__ g,
+                                                            float* __restrict__ dx, int64_t C,
+                                                            const float* rowscale, float rsc) {
+  __shared__ double dl[SM_NT / 64];
+  const int64_t r = blockIdx.x;
+  const float* yr = y + r * C;
+  const float* gr = g + r * C;
+  float* dr = dx + r * C;
+  double s = 0.0;
+  for (int64_t c = threadIdx.x; c < C; c += SM_NT) s += (double)(gr[c] * yr[c]);
+  const float sf = (float)block_sum<SM_NT>(s, dl);
+  const bool scaled = rowscale != nullptr || rsc != 0.0f;
+  const float k = rowscale != nullptr ? rowscale[r] : rsc;
+  for (int64_t c = threadIdx.x; c < C; c += SM_NT) {
+    float o = yr[c] * (gr[c] - sf);
+    if (scaled) o = o + k * yr[c];
+    dr[c] = o;
+  }
+}
+
+// LOG_SUM_EXP gradient g_r * exp(x - lse_r) (ReductionGradientRules.java:213-224).
+__global__ void lse_bwd_kernel(const float* __restrict__ x, const float* __restrict__ lse,
+                               const float* g, float gconst, float* __restrict__ dx, int64_t R,
+                               int64_t C) {
+  const int64_t n = R * C;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / C;
+    const float gr = g != nullptr ? g[r] : gconst;
+    dx[i] = gr * (float)exp((double)(x[i] - lse[r]));
+  }
+}
+
+// ---- MSE (CpuLossReferenceKernel.java:67-87, LossGradientRules.java:77-97) ----
+constexpr int MSE_BLOCKS = 1024;
+__global__ void __launch_bounds__(256) mse_pass1(const float* __restrict__ p,
+                                                 const float* __restrict__ t,
+                                                 float* __restrict__ grad, int64_t n, float gn,
+                                                 double* part) {
+  __shared__ double dl[4];
+  double s = 0.0;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+    const float d = p[i] - t[i];
+    const float sq = d * d;
+    s += (double)sq;
+    if (grad != nullptr) {
+      const float twice = d * 2.0f;
+      grad[i] = twice * gn;
+    }
+  }
+  s = block_sum<256>(s, dl);
+  if (threadIdx.x == 0) part[blockIdx.x] = s;
+}
+__global__ void __launch_bounds__(256) mse_pass2(const double* part, int P, int64_t n,
+                                                 float* loss) {
+  __shared__ double dl[4];
+  double s = 0.0;
+  for (int i = threadIdx.x; i < P; i += 256) s += part[i];
+  s = block_sum<256>(s, dl);
+  if (threadIdx.x == 0) {
+    // MEAN finalization divides the binary32 sum by the exact count before one final rounding.
+    const float sf = (float)s;
+    loss[0] = (float)((double)sf / (double)n);
+  }
+}
+
+// ---- Index categorical cross-entropy (CpuLossReferenceKernel.java:196-218,261-288;
+//      LossGradientRules.java:172-240). One wave per sample row. ----
+template <typename T>
+__global__ void __launch_bounds__(256) ce_pass1(const float* __restrict__ logits,
+                                                const T* __restrict__ target, int64_t R,
+                                                int64_t C, int has_ignore, int64_t ignore,
+                                                double* part, uint32_t* status) {
+  __shared__ double dl[4];
+  __shared__ double dc[4];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t r = (int64_t)blockIdx.x * 4 + w;
+  double loss = 0.0, count = 0.0;
+  if (r < R) {
+    const int64_t t = (int64_t)target[r];
+    const bool ignored = has_ignore && t == ignore;
+    if (!ignored) {
+      if (t < 0 || t >= C) {
+        if (lane == 0) atomicOr(status, (uint32_t)DEV_INDEX_OUT_OF_BOUNDS);
+      } else {
+        const float* row = logits + r * C;
+        // maximum by '>' (a NaN logit never becomes the maximum), as the loss oracle does
+        float m = -INFINITY;
+        for (int64_t c = lane; c < C; c += 64) {
+          const float v = row[c];
+          if (v > m) m = v;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+          const float u = __shfl_xor(m, o, 64);
+          if (u > m) m = u;
+        }
+        double s = 0.0;
+        for (int64_t c = lane; c < C; c += 64) s += (double)(float)exp((double)(row[c] - m));
+        s = wave_sum(s);
+        const float lse = m + (float)log((double)(float)s);
+        loss = (double)(lse - row[t]);
+        count = 1.0;
+      }
+    }
+  }
+  if (lane != 0) { loss = 0.0; count = 0.0; }
+  if (lane == 0) { dl[w] = loss; dc[w] = count; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    part[2 * blockIdx.x] = ((dl[0] + dl[1]) + dl[2]) + dl[3];
+    part[2 * blockIdx.x + 1] = ((dc[0] + dc[1]) + dc[2]) + dc[3];
+  }
+}
+__global__ void __launch_bounds__(256) ce_pass2(double* part, int P, float* loss) {
+  __shared__ double dl[4];
+  double s = 0.0, c = 0.0;
+  for (int i = threadIdx.x; i < P; i += 256) {
+    s += part[2 * i];
+    c += part[2 * i + 1];
+  }
+  s = block_sum<256>(s, dl);
+  __syncthreads();
+  c = block_sum<256>(c, dl);
+  if (threadIdx.x == 0) {
+    loss[0] = (float)s / (float)c;
+    part[2 * P] = c;  // non-ignored sample count for the gradient pass
+  }
+}
+template <typename T>
+__global__ void __launch_bounds__(256) ce_grad(const float* __restrict__ logits,
+                                               const T* __restrict__ target, int64_t R, int64_t C,
+                                               int has_ignore, int64_t ignore, float g,
+                                               const double* count_ptr,
+                                               float* __restrict__ grad) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t r = (int64_t)blockIdx.x * 4 + w;
+  if (r >= R) return;
+  const int64_t t = (int64_t)target[r];
+  const float* row = logits + r * C;
+  float* gr = grad + r * C;
+  if (has_ignore && t == ignore) {
+    for (int64_t c = lane; c < C; c += 64) gr[c] = 0.0f;
+    return;
+  }
+  const float scale = g / (float)(*count_ptr);
+  const int64_t safe = t < 0 ? 0 : (t >= C ? C - 1 : t);
+  float m = -INFINITY;
+  for (int64_t c = lane; c < C; c += 64) m = java_max(m, row[c]);
+  m = wave_max(m);
+  double s = 0.0;
+  for (int64_t c = lane; c < C; c += 64) s += (double)(float)exp((double)(row[c] - m));
+  const float sum = (float)wave_sum(s);
+  for (int64_t c = lane; c < C; c += 64) {
+    const float prob = (float)exp((double)(row[c] - m)) / sum;
+    const float hot = c == safe ? 1.0f : 0.0f;
+    gr[c] = (prob - hot) * scale;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_softmax_fwd(const float* x, float* y, float* lse, int64_t R, int64_t C,
+                              int log_softmax, hipStream_t s) {
+  if (R <= 0) return hipSuccess;
+  const bool vec = C % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15u) == 0;
+  dim3 g((unsigned)R), b(SM_NT);
+  if (vec && C > 0 && C <= 1024)
+    hipLaunchKernelGGL(softmax_fwd_regs<1>, g, b, 0, s, x, y, lse, C, log_softmax);
+  else if (vec && C > 0 && C <= 2048)
+    hipLaunchKernelGGL(softmax_fwd_regs<2>, g, b, 0, s, x, y, lse, C, log_softmax);
+  else if (vec && C > 0 && C <= 4096)
+    hipLaunchKernelGGL(softmax_fwd_regs<4>, g, b, 0, s, x, y, lse, C, log_softmax);
+  else
+    hipLaunchKernelGGL(softmax_fwd_stream, g, b, 0, s, x, y, lse, C, log_softmax);
+  return hipGetLastError();
+}
+
+hipError_t launch_softmax_bwd(const float* y, const float* g, float* dx, int64_t R, int64_t C,
+                              const float* rowscale, float rowscale_const, hipStream_t s) {
+  if (R <= 0) return hipSuccess;
+  const bool vec = C % 4 == 0 &&
+      ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(g) |
+        reinterpret_cast<uintptr_t>(dx)) & 15u) == 0;
+  dim3 gr((unsigned)R), b(SM_NT);
+  if (vec && C > 0 && C <= 1024)
+    hipLaunchKernelGGL(softmax_bwd_regs<1>, gr, b, 0, s, y, g, dx, C, rowscale, rowscale_const);
+  else if (vec && C > 0 && C <= 2048)
+    hipLaunchKernelGGL(softmax_bwd_regs<2>, gr, b, 0, s, y, g, dx, C, rowscale, rowscale_const);
+  else if (vec && C > 0 && C <= 4096)
+    hipLaunchKernelGGL(softmax_bwd_regs<4>, gr, b, 0, s, y, g, dx, C, rowscale, rowscale_const);
+  else
+    hipLaunchKernelGGL(softmax_bwd_stream, gr, b, 0, s, y, g, dx, C, rowscale, rowscale_const);
+  return hipGetLastError();
+}
+
+hipError_t launch_lse_bwd(const float* x, const float* lse, const float* g, float gconst,
+                          float* dx, int64_t R, int64_t C, hipStream_t s) {
+  const int64_t n = R * C;
+  if (n <= 0) return hipSuccess;
+  const unsigned blocks = (unsigned)std::min<int64_t>(65536, (n + 255) / 256);
+  hipLaunchKernelGGL(lse_bwd_kernel, dim3(blocks), dim3(256), 0, s, x, lse, g, gconst, dx, R, C);
+  return hipGetLastError();
+}
+
+int64_t mse_partial_doubles(int64_t) { return MSE_BLOCKS; }
+hipError_t launch_mse(const float* p, const float* t, float* loss, float* grad, int64_t n,
+                      float g, double* partial, hipStream_t s) {
+  const unsigned blocks = (unsigned)std::min<int64_t>(MSE_BLOCKS, std::max<int64_t>(1, (n + 1023) / 1024));
+  // restore(g) for MEAN: g / count with the count an exact binary32 sum of ones.
+  const float gn = g / (float)n;
+  hipLaunchKernelGGL(mse_pass1, dim3(blocks), dim3(256), 0, s, p, t, grad, n, gn, partial);
+  hipLaunchKernelGGL(mse_pass2, dim3(1), dim3(256), 0, s, (const double*)partial, (int)blocks, n, loss);
+  return hipGetLastError();
+}
+
+int64_t index_ce_partial_doubles(int64_t R) { return 2 * ((R + 3) / 4) + 2; }
+hipError_t launch_index_ce(const float* logits, const void* target, int target_is_64,
+                           float* loss, float* grad, int64_t R, int64_t C, int has_ignore,
+                           int64_t ignore_index, float g, double* partial, uint32_t* status,
+                           hipStream_t s) {
+  if (R <= 0) return hipSuccess;
+  const unsigned blocks = (unsigned)((R + 3) / 4);
+  if (target_is_64)
+    hipLaunchKernelGGL(ce_pass1<int64_t>, dim3(blocks), dim3(256), 0, s, logits,
+                       (const int64_t*)target, R, C, has_ignore, ignore_index, partial, status);
+  else
+    hipLaunchKernelGGL(ce_pass1<int32_t>, dim3(blocks), dim3(256), 0, s, logits,
+                       (const int32_t*)target, R, C, has_ignore, ignore_index, partial, status);
+  hipLaunchKernelGGL(ce_pass2, dim3(1), dim3(256), 0, s, partial, (int)blocks, loss);
+  if (grad != nullptr) {
+    const double* count = partial + 2 * blocks;
+    if (target_is_64)
+      hipLaunchKernelGGL(ce_grad<int64_t>, dim3(blocks), dim3(256), 0, s, logits,
+                         (const int64_t*)target, R, C, has_ignore, ignore_index, g, count, grad);
+    else
+      hipLaunchKernelGGL(ce_grad<int32_t>, dim3(blocks), dim3(256), 0, s, logits,
+                         (const int32_t*)target, R, C, has_ignore, ignore_index, g, count, grad);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace shk

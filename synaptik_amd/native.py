@@ -1,0 +1,294 @@
+"""ctypes binding of libsynaptik_hip.so: the host-side mirror of the reference's FFM binding.
+
+Mirrors `MetalNativeApi.Ffm` (modules/backend/metal/src/main/java/io/github/pho001/synaptik/
+backend/metal/MetalNativeApi.java:3582-3700): the library is looked up once, its ABI version is
+checked, every call returns an int32 status, and non-OK statuses become exceptions with the
+same meaning as the Metal mapping (MetalNativeApi.java:482-507): invalid argument / range ->
+IllegalArgument-like ValueError, allocation -> MemoryError, arithmetic -> ArithmeticError, the
+rest -> HipBackendError.
+
+There is deliberately no CPU fallback: if the library is missing, loading fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import numpy as np
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "libsynaptik_hip.so"
+ABI_VERSION = 1
+
+STATUS_NAMES = {
+    0: "OK",
+    1: "INVALID_ARGUMENT",
+    2: "NO_DEVICE",
+    3: "NO_COMMAND_QUEUE",
+    4: "ALLOCATION_FAILED",
+    5: "RANGE_OUT_OF_BOUNDS",
+    6: "COPY_FAILED",
+    7: "INTERNAL_ERROR",
+    8: "UNSUPPORTED_SHAPE",
+    9: "GRAPH_COMPILATION_FAILED",
+    10: "INCOMPATIBLE_RESOURCE",
+    11: "EXECUTION_FAILED",
+    12: "KERNEL_COMPILATION_FAILED",
+    13: "UNSUPPORTED_OPERATION",
+    14: "DEVICE_ERROR",
+    15: "ARITHMETIC",
+    16: "INDEX_OUT_OF_BOUNDS",
+}
+
+EXPORTED_SYMBOLS = (
+    "shk_hip_abi_version",
+    "shk_hip_last_error",
+    "shk_hip_context_create",
+    "shk_hip_context_release",
+    "shk_hip_device_info",
+    "shk_hip_buffer_create",
+    "shk_hip_buffer_wrap",
+    "shk_hip_buffer_release",
+    "shk_hip_buffer_upload",
+    "shk_hip_buffer_download",
+    "shk_hip_buffer_device_pointer",
+    "shk_hip_program_create",
+    "shk_hip_program_release",
+    "shk_hip_program_run",
+    "shk_hip_program_arena_bytes",
+    "shk_hip_program_set_profiling",
+    "shk_hip_program_step_times",
+    "shk_hip_program_step_count",
+)
+
+
+class HipBackendError(RuntimeError):
+    """A native status other than the argument, allocation and arithmetic classes."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+
+
+class HipInvalidArgument(HipBackendError, ValueError):
+    pass
+
+
+class HipAllocationError(HipBackendError, MemoryError):
+    pass
+
+
+class HipArithmeticError(HipBackendError, ArithmeticError):
+    pass
+
+
+class HipIndexError(HipBackendError, ValueError):
+    """Index target out of bounds (Java: IllegalArgumentException)."""
+
+
+_lib = None
+_lib_lock = threading.Lock()
+
+
+def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
+    """Loads the library once and checks its ABI version. Raises if it is absent."""
+    global _lib
+    with _lib_lock:
+        if _lib is not None:
+            return _lib
+        p = Path(path) if path is not None else LIBRARY_PATH
+        if not p.exists():
+            raise FileNotFoundError(
+                f"{p} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`"
+            )
+        lib = ctypes.CDLL(str(p))
+        vp = ctypes.c_void_p
+        u64 = ctypes.c_uint64
+        i32 = ctypes.c_int32
+        u32 = ctypes.c_uint32
+        sig = {
+            "shk_hip_abi_version": (u32, []),
+            "shk_hip_last_error": (i32, [ctypes.c_char_p, u64]),
+            "shk_hip_context_create": (i32, [i32, ctypes.POINTER(vp)]),
+            "shk_hip_context_release": (i32, [vp]),
+            "shk_hip_device_info": (i32, [vp, ctypes.POINTER(i32), ctypes.POINTER(i32),
+                                          ctypes.POINTER(u64), ctypes.c_char_p, u64]),
+            "shk_hip_buffer_create": (i32, [vp, u64, ctypes.POINTER(vp)]),
+            "shk_hip_buffer_wrap": (i32, [vp, vp, u64, ctypes.POINTER(vp)]),
+            "shk_hip_buffer_release": (i32, [vp]),
+            "shk_hip_buffer_upload": (i32, [vp, u64, vp, u64]),
+            "shk_hip_buffer_download": (i32, [vp, u64, vp, u64]),
+            "shk_hip_buffer_device_pointer": (i32, [vp, ctypes.POINTER(vp)]),
+            "shk_hip_program_create": (i32, [vp, vp, u64, ctypes.POINTER(vp)]),
+            "shk_hip_program_release": (i32, [vp]),
+            "shk_hip_program_run": (i32, [vp, u32, ctypes.POINTER(vp), u32, ctypes.POINTER(vp)]),
+            "shk_hip_program_arena_bytes": (i32, [vp, ctypes.POINTER(u64)]),
+            "shk_hip_program_set_profiling": (i32, [vp, i32]),
+            "shk_hip_program_step_times": (i32, [vp, ctypes.POINTER(ctypes.c_double), u32,
+                                                 ctypes.POINTER(u64)]),
+            "shk_hip_program_step_count": (i32, [vp, ctypes.POINTER(u32)]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        version = lib.shk_hip_abi_version()
+        if version != ABI_VERSION:
+            raise HipBackendError(7, f"ABI version {version} != expected {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def _last_error(lib) -> str:
+    buf = ctypes.create_string_buffer(512)
+    lib.shk_hip_last_error(buf, 512)
+    return buf.value.decode(errors="replace")
+
+
+def check(lib, status: int) -> None:
+    """Maps a native status to the exception class the Java binding would throw."""
+    if status == 0:
+        return
+    msg = _last_error(lib)
+    if status in (1, 5, 8, 10):
+        raise HipInvalidArgument(status, msg)
+    if status == 4:
+        raise HipAllocationError(status, msg)
+    if status == 15:
+        raise HipArithmeticError(status, msg)
+    if status == 16:
+        raise HipIndexError(status, msg)
+    raise HipBackendError(status, msg)
+
+
+class HipContext:
+    """One device and one stream (`shk_hip_context_create`)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        h = ctypes.c_void_p()
+        check(self.lib, self.lib.shk_hip_context_create(device, ctypes.byref(h)))
+        self.handle = h
+        self.device = device
+
+    def device_info(self) -> dict:
+        cu = ctypes.c_int32()
+        clk = ctypes.c_int32()
+        mem = ctypes.c_uint64()
+        name = ctypes.create_string_buffer(128)
+        check(self.lib, self.lib.shk_hip_device_info(self.handle, ctypes.byref(cu), ctypes.byref(clk),
+                                                     ctypes.byref(mem), name, 128))
+        return {"compute_units": cu.value, "clock_khz": clk.value, "memory_bytes": mem.value,
+                "arch": name.value.decode()}
+
+    def buffer(self, nbytes: int) -> "HipBuffer":
+        return HipBuffer(self, nbytes)
+
+    def upload(self, array: np.ndarray) -> "HipBuffer":
+        a = np.ascontiguousarray(array)
+        b = HipBuffer(self, a.nbytes)
+        b.upload(a)
+        return b
+
+    def close(self) -> None:
+        if self.handle:
+            check(self.lib, self.lib.shk_hip_context_release(self.handle))
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+class HipBuffer:
+    """Device buffer handle (`shk_hip_buffer_*`); released exactly once."""
+
+    def __init__(self, ctx: HipContext, nbytes: int, wrap_pointer: int | None = None):
+        self.ctx = ctx
+        self.lib = ctx.lib
+        self.nbytes = int(nbytes)
+        h = ctypes.c_void_p()
+        if wrap_pointer is None:
+            check(self.lib, self.lib.shk_hip_buffer_create(ctx.handle, self.nbytes, ctypes.byref(h)))
+        else:
+            check(self.lib, self.lib.shk_hip_buffer_wrap(ctx.handle, ctypes.c_void_p(wrap_pointer),
+                                                         self.nbytes, ctypes.byref(h)))
+        self.handle = h
+
+    def upload(self, array: np.ndarray, offset: int = 0) -> None:
+        a = np.ascontiguousarray(array)
+        check(self.lib, self.lib.shk_hip_buffer_upload(self.handle, offset, a.ctypes.data, a.nbytes))
+
+    def download(self, dtype=np.float32, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dt = np.dtype(dtype)
+        n = (self.nbytes - offset) // dt.itemsize if count is None else count
+        out = np.empty(n, dtype=dt)
+        check(self.lib, self.lib.shk_hip_buffer_download(self.handle, offset, out.ctypes.data, out.nbytes))
+        return out
+
+    def device_pointer(self) -> int:
+        p = ctypes.c_void_p()
+        check(self.lib, self.lib.shk_hip_buffer_device_pointer(self.handle, ctypes.byref(p)))
+        return p.value or 0
+
+    def close(self) -> None:
+        if self.handle:
+            check(self.lib, self.lib.shk_hip_buffer_release(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class HipProgram:
+    """A created program (`shk_hip_program_create`) bound to a context."""
+
+    def __init__(self, ctx: HipContext, image: bytes):
+        self.ctx = ctx
+        self.lib = ctx.lib
+        buf = ctypes.create_string_buffer(image, len(image))
+        h = ctypes.c_void_p()
+        check(self.lib, self.lib.shk_hip_program_create(ctx.handle, buf, len(image), ctypes.byref(h)))
+        self.handle = h
+
+    def run(self, inputs, outputs) -> None:
+        ins = (ctypes.c_void_p * max(1, len(inputs)))(*[b.handle.value for b in inputs])
+        outs = (ctypes.c_void_p * max(1, len(outputs)))(*[b.handle.value for b in outputs])
+        check(self.lib, self.lib.shk_hip_program_run(self.handle, len(inputs), ins, len(outputs), outs))
+
+    def arena_bytes(self) -> int:
+        v = ctypes.c_uint64()
+        check(self.lib, self.lib.shk_hip_program_arena_bytes(self.handle, ctypes.byref(v)))
+        return v.value
+
+    def step_count(self) -> int:
+        v = ctypes.c_uint32()
+        check(self.lib, self.lib.shk_hip_program_step_count(self.handle, ctypes.byref(v)))
+        return v.value
+
+    def set_profiling(self, enabled: bool) -> None:
+        check(self.lib, self.lib.shk_hip_program_set_profiling(self.handle, 1 if enabled else 0))
+
+    def step_times(self):
+        n = self.step_count()
+        arr = (ctypes.c_double * max(1, n))()
+        runs = ctypes.c_uint64()
+        check(self.lib, self.lib.shk_hip_program_step_times(self.handle, arr, n, ctypes.byref(runs)))
+        return list(arr)[:n], runs.value
+
+    def close(self) -> None:
+        if self.handle:
+            check(self.lib, self.lib.shk_hip_program_release(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,106 @@
+"""GEMM parity on the GPU against the no-FMA sequential oracle (CpuMatmulReferenceKernel).
+
+Integer-valued operands in [-3, 3] make every partial sum exact in binary32, so the MFMA GEMM
+must be bit-identical to the oracle whatever its reduction order; N(0,1) operands are checked
+against the oracle within the bound |err| <= gamma_K * sum|a||b| (gamma_K = K u / (1 - K u)).
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle
+from synaptik_amd.program import ProgramBuilder
+from tests.gpu_helpers import run_program
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 1, 1), (7, 5, 3), (64, 64, 16), (256, 64, 16), (256, 1, 64), (130, 70, 33),
+          (1024, 10, 1024), (257, 513, 129), (512, 512, 512), (1024, 1024, 784)]
+
+
+def _gemm_case(ctx, A, B, M, N, K, ta, tb, bias=None, act=None, aux=None, act_grad=False):
+    pb = ProgramBuilder()
+    sa = pb.input(A.size)
+    sb = pb.input(B.size)
+    inputs = [A, B]
+    sbias = saux = None
+    if bias is not None:
+        sbias = pb.input(bias.size)
+        inputs.append(bias)
+    if aux is not None:
+        saux = pb.input(aux.size)
+        inputs.append(aux)
+    sc = pb.output(M * N)
+    pb.gemm(sa, sb, sc, M, N, K, trans_a=ta, trans_b=tb, bias=sbias, act=act, aux=saux,
+            act_grad=act_grad)
+    (C,) = run_program(ctx, pb, inputs, [sc])
+    return C.reshape(M, N)
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_gemm_integer_operands_bit_exact(ctx, shape, ta, tb):
+    M, N, K = shape
+    rng = np.random.default_rng(M * 7919 + N * 31 + K)
+    A = rng.integers(-3, 4, size=(K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.integers(-3, 4, size=(N, K) if tb else (K, N)).astype(np.float32)
+    C = _gemm_case(ctx, A, B, M, N, K, ta, tb)
+    ref = oracle.matmul(A, B, trans_a=ta, trans_b=tb)
+    assert np.array_equal(C, ref), f"max diff {np.abs(C - ref).max()}"
+
+
+@pytest.mark.parametrize("ta,tb", [(False, True), (False, False), (True, False)])
+@pytest.mark.parametrize("shape", [(300, 200, 1000), (1024, 1024, 1024)])
+def test_gemm_gaussian_within_bound(ctx, shape, ta, tb):
+    M, N, K = shape
+    rng = np.random.default_rng(5)
+    A = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    C = _gemm_case(ctx, A, B, M, N, K, ta, tb)
+    ref = oracle.matmul(A, B, trans_a=ta, trans_b=tb)
+    Ad = np.abs(A.T if ta else A).astype(np.float64)
+    Bd = np.abs(B.T if tb else B).astype(np.float64)
+    u = 2.0 ** -24
+    gamma = K * u / (1 - K * u)
+    bound = 2 * gamma * (Ad @ Bd) + 1e-30  # GPU and oracle each within gamma of the exact value
+    assert (np.abs(C.astype(np.float64) - ref) <= bound).all()
+    rel = np.linalg.norm(C - ref) / np.linalg.norm(ref)
+    assert rel < 1e-5
+
+
+@pytest.mark.parametrize("act", ["relu", "tanh", "sigmoid", None])
+def test_gemm_bias_activation_epilogue(ctx, act):
+    M, N, K = 200, 96, 64
+    rng = np.random.default_rng(11)
+    X = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    W = rng.integers(-3, 4, size=(N, K)).astype(np.float32) * np.float32(0.125)
+    b = rng.standard_normal(N).astype(np.float32)
+    Y = _gemm_case(ctx, X, W, M, N, K, False, True, bias=b, act=act)
+    ref = oracle.linear_forward(X, W, b, act)
+    assert np.array_equal(Y, ref)
+
+
+@pytest.mark.parametrize("act", ["relu", "tanh", "sigmoid"])
+def test_gemm_activation_gradient_epilogue(ctx, act):
+    M, N, K = 130, 72, 48  # dX[M,N] = dZ[M,K] . W[K,N], then act_grad with y = aux
+    rng = np.random.default_rng(12)
+    dZ = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    W = rng.integers(-3, 4, size=(K, N)).astype(np.float32)
+    y = oracle.activation(act, rng.standard_normal((M, N)).astype(np.float32))
+    y[0, :5] = 0.0
+    out = _gemm_case(ctx, dZ, W, M, N, K, False, False, aux=y, act=act, act_grad=True)
+    ref = oracle.activation_grad(act, oracle.matmul(dZ, W), y)
+    assert np.array_equal(out, ref)
+
+
+def test_gemm_empty_contraction_is_positive_zero(ctx):
+    M, N = 5, 7
+    A = np.zeros((M, 0), np.float32)
+    B = np.zeros((0, N), np.float32)
+    pb = ProgramBuilder()
+    sa = pb.input(1)
+    sb = pb.input(1)
+    sc = pb.output(M * N)
+    pb.gemm(sa, sb, sc, M, N, 0)
+    (C,) = run_program(ctx, pb, [np.zeros(1, np.float32), np.zeros(1, np.float32)], [sc])
+    assert np.array_equal(C.view(np.uint32), np.zeros(M * N, np.uint32))

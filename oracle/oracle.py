@@ -60,7 +60,8 @@ def lib():
             "shko_softmax_grad_rows": (None, [F32P, F32P, F32P, i64, i64]),
             "shko_logsumexp_grad_rows": (None, [F32P, F32P, F32P, F32P, i64, i64]),
             "shko_mse_mean": (f32, [F32P, F32P, i64]),
-            "shko_mse_grad": (None, [F32P, F32P, F32P, i64, f32]),
+            "shko_mse_sum": (f32, [F32P, F32P, i64]),
+            "shko_mse_grad": (None, [F32P, F32P, F32P, i64, f32, i32]),
             "shko_index_ce_mean": (i32, [F32P, I64P, i64, i64, i32, i64, F32P]),
             "shko_index_ce_grad": (None, [F32P, I64P, F32P, i64, i64, i32, i64, f32]),
             "shko_sgd_stage": (i32, [F32P, F32P, F32P, F32P, F32P, i64, f32, f32, f32, f32, i32,
@@ -174,10 +175,15 @@ def mse_mean(p, t) -> np.float32:
     return np.float32(lib().shko_mse_mean(_f(p), _f(t), p.size))
 
 
-def mse_grad(p, t, g=1.0) -> np.ndarray:
+def mse_sum(p, t) -> np.float32:
+    p, t = _c(p).ravel(), _c(t).ravel()
+    return np.float32(lib().shko_mse_sum(_f(p), _f(t), p.size))
+
+
+def mse_grad(p, t, g=1.0, reduction="mean") -> np.ndarray:
     p, t = _c(p), _c(t)
     d = np.empty_like(p)
-    lib().shko_mse_grad(_f(p), _f(t), _f(d), p.size, float(g))
+    lib().shko_mse_grad(_f(p), _f(t), _f(d), p.size, float(g), int(reduction == "sum"))
     return d
 
 
@@ -239,11 +245,13 @@ class OracleMLP:
                dict(kind="adam"/"adamw", lr, beta1, beta2, eps, weight_decay).
     """
 
-    def __init__(self, weights, biases, acts, loss, optimizer):
+    def __init__(self, weights, biases, acts, loss, optimizer, reduction="mean"):
         self.W = [np.array(w, np.float32) for w in weights]
-        self.b = [np.array(b, np.float32) for b in biases]
+        self.b = [np.array(b, np.float32) for b in biases if b is not None]
+        self.has_bias = [b is not None for b in biases]
         self.acts = list(acts)
         self.loss = loss
+        self.reduction = reduction
         self.opt = dict(optimizer)
         self.m = [np.zeros_like(w) for w in self.W] + [np.zeros_like(b) for b in self.b]
         self.v = [np.zeros_like(w) for w in self.W] + [np.zeros_like(b) for b in self.b]
@@ -251,16 +259,17 @@ class OracleMLP:
 
     def forward(self, x):
         xs = [_c(x)]
-        for W, b, a in zip(self.W, self.b, self.acts):
-            xs.append(linear_forward(xs[-1], W, b, a))
+        bi = iter(self.b)
+        for W, hb, a in zip(self.W, self.has_bias, self.acts):
+            xs.append(linear_forward(xs[-1], W, next(bi) if hb else None, a))
         return xs
 
     def gradients(self, x, y):
         xs = self.forward(x)
         pred = xs[-1]
         if self.loss == "mse":
-            loss = mse_mean(pred, y)
-            dz = mse_grad(pred, y)
+            loss = mse_mean(pred, y) if self.reduction == "mean" else mse_sum(pred, y)
+            dz = mse_grad(pred, y, reduction=self.reduction)
         else:
             loss = index_ce_mean(pred, y)
             dz = index_ce_grad(pred, y)
@@ -268,7 +277,7 @@ class OracleMLP:
         gW, gb = [None] * L, [None] * L
         for l in reversed(range(L)):
             gW[l] = matmul(dz, xs[l], trans_a=True)
-            gb[l] = colsum(dz)
+            gb[l] = colsum(dz) if self.has_bias[l] else None
             if l > 0:
                 dx = matmul(dz, self.W[l])
                 dz = activation_grad(self.acts[l - 1], dx, xs[l])
@@ -278,7 +287,7 @@ class OracleMLP:
         """One training step; returns the objective. Raises ArithmeticError without commit."""
         loss, gW, gb, _ = self.gradients(x, y)
         params = self.W + self.b
-        grads = gW + gb
+        grads = gW + [g for g in gb if g is not None]
         o = self.opt
         staged = []
         for i, (p, g) in enumerate(zip(params, grads)):

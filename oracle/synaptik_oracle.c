@@ -373,10 +373,21 @@ float shko_mse_mean(const float* p, const float* t, int64_t n) {
   return shko_exact_quotient(sum, n);
 }
 
+/* meanSquaredError(float[], float[], SUM): the sequential binary32 sum itself. */
+float shko_mse_sum(const float* p, const float* t, int64_t n) {
+  float sum = 0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    float d = p[i] - t[i];
+    float sq = d * d;
+    sum += sq;
+  }
+  return sum;
+}
+
 /* MSE MEAN gradient ((p - t) * 2) * (g / count) (LossGradientRules.java:77-97 with restore()
  * dividing the expanded cotangent by the exact element count). */
-void shko_mse_grad(const float* p, const float* t, float* grad, int64_t n, float g) {
-  const float gn = g / (float)n;
+void shko_mse_grad(const float* p, const float* t, float* grad, int64_t n, float g, int sum) {
+  const float gn = sum ? g : g / (float)n;
   for (int64_t i = 0; i < n; ++i) {
     float d = p[i] - t[i];
     float twice = d * 2.0f;

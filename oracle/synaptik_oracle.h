@@ -22,7 +22,8 @@ void shko_softmax_grad_rows(const float* Y, const float* G, float* DX, int64_t R
 void shko_logsumexp_grad_rows(const float* X, const float* lse, const float* g, float* DX,
                               int64_t R, int64_t C);
 float shko_mse_mean(const float* p, const float* t, int64_t n);
-void shko_mse_grad(const float* p, const float* t, float* grad, int64_t n, float g);
+float shko_mse_sum(const float* p, const float* t, int64_t n);
+void shko_mse_grad(const float* p, const float* t, float* grad, int64_t n, float g, int sum);
 int shko_index_ce_mean(const float* logits, const int64_t* target, int64_t R, int64_t C,
                        int has_ignore, int64_t ignore, float* loss);
 void shko_index_ce_grad(const float* logits, const int64_t* target, float* grad, int64_t R,

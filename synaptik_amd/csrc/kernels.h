@@ -63,9 +63,10 @@ hipError_t launch_softmax_bwd(const float* y, const float* g, float* dx, int64_t
 hipError_t launch_lse_bwd(const float* x, const float* lse, const float* g, float gconst,
                           float* dx, int64_t R, int64_t C, hipStream_t s);
 
-// Mean squared error over n elements: loss = sum((p-t)^2) / n; grad = ((p-t)*2) * (g/n).
+// Squared error over n elements, MEAN (loss = sum((p-t)^2) / n, grad = ((p-t)*2) * (g/n)) or
+// SUM (loss = sum((p-t)^2), grad = ((p-t)*2) * g).
 hipError_t launch_mse(const float* p, const float* t, float* loss, float* grad, int64_t n,
-                      float g, double* partial, hipStream_t s);
+                      float g, int reduction_sum, double* partial, hipStream_t s);
 int64_t mse_partial_doubles(int64_t n);
 
 // Index categorical cross-entropy with logits [R,C], integer targets [R] (int32 or int64),

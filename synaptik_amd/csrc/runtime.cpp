@@ -335,7 +335,8 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
     }
     case OP_MSE: {
       const int64_t n = a[0];
-      if (n <= 0) return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: MSE needs elements", idx);
+      if (n <= 0 || (a[1] != 0 && a[1] != 1))
+        return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid MSE", idx);
       if (!v.slot_ok(s[0], false, "P") || !v.slot_ok(s[1], false, "T") || !v.slot_ok(s[2], false, "loss") ||
           !v.slot_ok(s[3], true, "grad") || !v.holds(s[0], n, DT_F32, "P") || !v.holds(s[1], n, DT_F32, "T") ||
           !v.holds(s[2], 1, DT_F32, "loss") || !v.holds(s[3], n, DT_F32, "grad") ||
@@ -456,7 +457,7 @@ hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipSt
                                  r.farg[0], b.get<float>(s[3]), a[0], a[1], stream);
     case OP_MSE:
       return shk::launch_mse(b.get<const float>(s[0]), b.get<const float>(s[1]), b.get<float>(s[2]),
-                             b.get<float>(s[3]), a[0], r.farg[0], pr.scratch, stream);
+                             b.get<float>(s[3]), a[0], r.farg[0], (int)a[1], pr.scratch, stream);
     case OP_CE_INDEX:
       return shk::launch_index_ce(b.get<const float>(s[0]), b.get<const void>(s[1]), (int)a[2],
                                   b.get<float>(s[2]), b.get<float>(s[3]), a[0], a[1], (int)a[3], a[4],

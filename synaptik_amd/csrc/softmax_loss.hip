@@ -259,7 +259,7 @@ __global__ void __launch_bounds__(256) mse_pass1(const float* __restrict__ p,
   if (threadIdx.x == 0) part[blockIdx.x] = s;
 }
 __global__ void __launch_bounds__(256) mse_pass2(const double* part, int P, int64_t n,
-                                                 float* loss) {
+                                                 int reduction_sum, float* loss) {
   __shared__ double dl[4];
   double s = 0.0;
   for (int i = threadIdx.x; i < P; i += 256) s += part[i];
@@ -267,7 +267,7 @@ __global__ void __launch_bounds__(256) mse_pass2(const double* part, int P, int6
   if (threadIdx.x == 0) {
     // MEAN finalization divides the binary32 sum by the exact count before one final rounding.
     const float sf = (float)s;
-    loss[0] = (float)((double)sf / (double)n);
+    loss[0] = reduction_sum ? sf : (float)((double)sf / (double)n);
   }
 }
 
@@ -412,12 +412,13 @@ hipError_t launch_lse_bwd(const float* x, const float* lse, const float* g, floa
 
 int64_t mse_partial_doubles(int64_t) { return MSE_BLOCKS; }
 hipError_t launch_mse(const float* p, const float* t, float* loss, float* grad, int64_t n,
-                      float g, double* partial, hipStream_t s) {
+                      float g, int reduction_sum, double* partial, hipStream_t s) {
   const unsigned blocks = (unsigned)std::min<int64_t>(MSE_BLOCKS, std::max<int64_t>(1, (n + 1023) / 1024));
-  // restore(g) for MEAN: g / count with the count an exact binary32 sum of ones.
-  const float gn = g / (float)n;
+  // restore(g): MEAN divides g by the count (an exact binary32 sum of ones); SUM expands g.
+  const float gn = reduction_sum ? g : g / (float)n;
   hipLaunchKernelGGL(mse_pass1, dim3(blocks), dim3(256), 0, s, p, t, grad, n, gn, partial);
-  hipLaunchKernelGGL(mse_pass2, dim3(1), dim3(256), 0, s, (const double*)partial, (int)blocks, n, loss);
+  hipLaunchKernelGGL(mse_pass2, dim3(1), dim3(256), 0, s, (const double*)partial, (int)blocks, n,
+                     reduction_sum, loss);
   return hipGetLastError();
 }
 

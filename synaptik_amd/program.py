@@ -171,8 +171,8 @@ class ProgramBuilder:
     def lse_bwd(self, X, lse, dX, R, C, *, g=None, gconst=1.0) -> Step:
         return self._add(OP_LSE_BWD, [X, lse, g, dX], [R, C], [gconst])
 
-    def mse(self, P, T, loss, n, *, grad=None, g=1.0) -> Step:
-        return self._add(OP_MSE, [P, T, loss, grad], [n], [g])
+    def mse(self, P, T, loss, n, *, grad=None, g=1.0, reduction="mean") -> Step:
+        return self._add(OP_MSE, [P, T, loss, grad], [n, {"mean": 0, "sum": 1}[reduction]], [g])
 
     def index_ce(self, logits, target, loss, R, C, *, grad=None, ignore_index=None, g=1.0) -> Step:
         is64 = 1 if (isinstance(target, Slot) and target.dtype == "i64") else 0

@@ -1,0 +1,364 @@
+"""Device-resident training for fully-connected networks on the HIP backend.
+
+Mirrors the reference's training surface for the MLP path:
+  * optimizer configurations `Sgd`, `Adam`, `AdamW` with the reference's validation
+    (modules/training/src/main/java/io/github/pho001/synaptik/training/Sgd.java:23-181,
+     Adam.java:194-286);
+  * `HipTrainingSession` ~ `TrainingSession` (TrainingSession.java:242-647): `open`, `run`
+    (GradientMode.RESET_AND_STEP), `optimizer_steps`, `state()` / `restore()` with byte-exact
+    parameter and optimizer slots (TrainingSession.java:680-760).
+
+Unlike the reference, whose optimizer runs on the host after downloading every gradient
+(TrainingSession.java:916-950, TrainingParameter.java:409-672), the whole step is ONE program:
+forward GEMMs with fused bias+activation, the loss and its gradient, the backward GEMMs (dX with
+the previous layer's activation gradient fused into the epilogue, dW written directly in [out,in]
+order), the bias column sums, and the transactional fused optimizer update. Parameters, slots and
+the completed-step counter stay in HBM; a run downloads only the objective.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Sequence
+
+import numpy as np
+
+from .native import HipBuffer, HipContext, HipProgram
+from .program import ProgramBuilder, Slot
+
+ACTIVATIONS = (None, "relu", "tanh", "sigmoid")
+
+
+# ---- optimizer configurations (immutable, validated like the reference records) ----
+@dataclass(frozen=True)
+class Sgd:
+    """SGD with optional momentum, dampening, coupled weight decay and Nesterov (Sgd.java:23-181)."""
+    learning_rate: float
+    momentum: float = 0.0
+    dampening: float = 0.0
+    weight_decay: float = 0.0
+    nesterov: bool = False
+
+    def __post_init__(self):
+        if not (math.isfinite(self.learning_rate) and self.learning_rate > 0):
+            raise ValueError(f"learning rate must be finite and positive: {self.learning_rate}")
+        if not (math.isfinite(self.momentum) and 0.0 <= self.momentum < 1.0):
+            raise ValueError(f"momentum must be finite and in [0, 1): {self.momentum}")
+        if not (math.isfinite(self.dampening) and 0.0 <= self.dampening <= 1.0):
+            raise ValueError(f"dampening must be finite and in [0, 1]: {self.dampening}")
+        if not (math.isfinite(self.weight_decay) and self.weight_decay >= 0.0):
+            raise ValueError(f"weight decay must be finite and non-negative: {self.weight_decay}")
+        if self.nesterov and (self.momentum <= 0.0 or self.dampening != 0.0):
+            raise ValueError("Nesterov requires positive momentum and zero dampening")
+
+
+@dataclass(frozen=True)
+class Adam:
+    """Adam with coupled L2 decay (Adam.java:194-286)."""
+    learning_rate: float
+    beta1: float = 0.9
+    beta2: float = 0.999
+    epsilon: float = 1e-8
+    weight_decay: float = 0.0
+
+    decoupled = False
+
+    def __post_init__(self):
+        if not (math.isfinite(self.learning_rate) and self.learning_rate > 0):
+            raise ValueError("learning rate must be finite and positive")
+        for name in ("beta1", "beta2"):
+            v = getattr(self, name)
+            if not (math.isfinite(v) and 0.0 <= v < 1.0):
+                raise ValueError(f"{name} must be finite and in [0, 1): {v}")
+        if not (math.isfinite(self.epsilon) and self.epsilon > 0):
+            raise ValueError("epsilon must be finite and positive")
+        if not (math.isfinite(self.weight_decay) and self.weight_decay >= 0):
+            raise ValueError("weight decay must be finite and non-negative")
+
+
+@dataclass(frozen=True)
+class AdamW(Adam):
+    """Adam with decoupled weight decay."""
+    decoupled = True
+
+
+# ---- model description ----
+@dataclass
+class Dense:
+    """One Linear layer y = act(x . W^T + b) with W stored [out, in] (Linear.java:48-370)."""
+    fan_in: int
+    fan_out: int
+    activation: str | None = None
+    bias: bool = True
+
+    def __post_init__(self):
+        if self.activation not in ACTIVATIONS:
+            raise ValueError(f"unsupported activation {self.activation}")
+        if self.fan_in <= 0 or self.fan_out <= 0:
+            raise ValueError("layer extents must be positive")
+
+
+@dataclass
+class MlpSpec:
+    layers: list[Dense]
+    loss: str = "mse"  # "mse" or "ce" (index categorical cross-entropy with logits)
+    reduction: str = "mean"  # loss reduction: "mean" or "sum" (MSE only)
+
+    def __post_init__(self):
+        if not self.layers:
+            raise ValueError("a network needs at least one layer")
+        for a, b in zip(self.layers, self.layers[1:]):
+            if a.fan_out != b.fan_in:
+                raise ValueError("consecutive layer extents differ")
+        if self.loss not in ("mse", "ce"):
+            raise ValueError(f"unsupported loss {self.loss}")
+        if self.reduction not in ("mean", "sum") or (self.loss == "ce" and self.reduction != "mean"):
+            raise ValueError(f"unsupported reduction {self.reduction}")
+
+    @staticmethod
+    def chain(widths: Sequence[int], hidden: str | None, loss: str = "mse",
+              output: str | None = None) -> "MlpSpec":
+        layers = []
+        for i, (a, b) in enumerate(zip(widths, widths[1:])):
+            last = i == len(widths) - 2
+            layers.append(Dense(a, b, output if last else hidden))
+        return MlpSpec(layers, loss)
+
+    def parameter_count(self) -> int:
+        return sum(l.fan_in * l.fan_out + (l.fan_out if l.bias else 0) for l in self.layers)
+
+
+def init_parameters(spec: MlpSpec, seed: int, scheme: str):
+    """Seeded initial weights: 'xavier_uniform' (bound sqrt(6/(fan_in+fan_out))) or
+    'he_normal' (sigma sqrt(2/fan_in)); biases zero (ParameterInitializers.java:269-372)."""
+    rng = np.random.default_rng(seed)
+    Ws, bs = [], []
+    for l in spec.layers:
+        if scheme == "xavier_uniform":
+            bound = math.sqrt(6.0 / (l.fan_in + l.fan_out))
+            W = rng.uniform(-bound, bound, size=(l.fan_out, l.fan_in))
+        elif scheme == "he_normal":
+            W = rng.standard_normal((l.fan_out, l.fan_in)) * math.sqrt(2.0 / l.fan_in)
+        else:
+            raise ValueError(f"unknown init scheme {scheme}")
+        Ws.append(W.astype(np.float32))
+        bs.append(np.zeros(l.fan_out, np.float32) if l.bias else None)
+    return Ws, bs
+
+
+# ---- lowering ----
+@dataclass
+class TrainingLayout:
+    """Slot handles of a lowered training program, in input-index order."""
+    weights: list[Slot] = field(default_factory=list)
+    biases: list[Slot] = field(default_factory=list)
+    first: list[Slot] = field(default_factory=list)    # momentum / first-moment slots
+    second: list[Slot] = field(default_factory=list)   # second-moment slots (Adam)
+    counter: Slot | None = None
+    x: Slot | None = None
+    y: Slot | None = None
+    loss: Slot | None = None
+    grads: list[Slot] = field(default_factory=list)
+
+
+def _optimizer_kind(opt) -> str:
+    if isinstance(opt, Sgd):
+        return "sgd"
+    if isinstance(opt, Adam):
+        return "adamw" if opt.decoupled else "adam"
+    raise TypeError(f"unsupported optimizer {opt!r}")
+
+
+def lower_training_step(spec: MlpSpec, batch: int, optimizer, *, label_dtype: str = "i64"):
+    """Lowers one training step of `spec` at `batch` rows to a program image.
+
+    Inputs (in order): W_1..W_L, b_1..b_L (INOUT), first-moment slots per tensor (INOUT, SGD
+    with momentum and Adam), second-moment slots (INOUT, Adam), completed-step counter (INOUT,
+    int64), x [batch, in], y ([batch, out] f32 for MSE; [batch] int for CE).
+    Output: objective [1].
+    """
+    kind = _optimizer_kind(optimizer)
+    pb = ProgramBuilder()
+    lay = TrainingLayout()
+    L = len(spec.layers)
+    for l in spec.layers:
+        lay.weights.append(pb.input(l.fan_in * l.fan_out, inout=True))
+    for l in spec.layers:
+        lay.biases.append(pb.input(l.fan_out, inout=True) if l.bias else None)
+    params = lay.weights + [b for b in lay.biases if b is not None]
+    has_first = kind != "sgd" or optimizer.momentum != 0.0
+    if has_first:
+        lay.first = [pb.input(p.count, inout=True) for p in params]
+    if kind != "sgd":
+        lay.second = [pb.input(p.count, inout=True) for p in params]
+    lay.counter = pb.input(1, "i64", inout=True)
+    lay.x = pb.input(batch * spec.layers[0].fan_in)
+    out_w = spec.layers[-1].fan_out
+    if spec.loss == "mse":
+        lay.y = pb.input(batch * out_w)
+    else:
+        lay.y = pb.input(batch, label_dtype)
+    lay.loss = pb.output(1)
+
+    # activations Y_l (internal); Y_0 is the input x
+    acts = [lay.x] + [pb.internal(batch * l.fan_out) for l in spec.layers]
+    widest = max(l.fan_out for l in spec.layers)
+    dz = [pb.internal(batch * widest), pb.internal(batch * widest)]
+    gW = [pb.internal(l.fan_in * l.fan_out) for l in spec.layers]
+    gb = [pb.internal(l.fan_out) if l.bias else None for l in spec.layers]
+    lay.grads = gW + [g for g in gb if g is not None]
+
+    # forward
+    for i, l in enumerate(spec.layers):
+        pb.gemm(acts[i], lay.weights[i], acts[i + 1], batch, l.fan_out, l.fan_in, trans_b=True,
+                bias=lay.biases[i], act=l.activation)
+    # objective and its cotangent (g = 1)
+    cur = dz[0]
+    if spec.loss == "mse":
+        if spec.layers[-1].activation is not None:
+            raise ValueError("the MSE head is lowered for an identity output layer")
+        pb.mse(acts[L], lay.y, lay.loss, batch * out_w, grad=cur, reduction=spec.reduction)
+    else:
+        if spec.layers[-1].activation is not None:
+            raise ValueError("cross-entropy consumes raw logits")
+        pb.index_ce(acts[L], lay.y, lay.loss, batch, out_w, grad=cur)
+    # backward
+    for i in reversed(range(L)):
+        l = spec.layers[i]
+        # dW[out,in] = dZ^T . X   (PERMUTE of X^T.dZ absorbed)
+        pb.gemm(cur, acts[i], gW[i], l.fan_out, l.fan_in, batch, trans_a=True)
+        if gb[i] is not None:
+            pb.colsum(cur, gb[i], batch, l.fan_out)
+        if i > 0:
+            nxt = dz[1] if cur is dz[0] else dz[0]
+            prev = spec.layers[i - 1]
+            # dZ_{i-1} = act_grad(dZ_i . W_i, Y_{i-1})
+            pb.gemm(cur, lay.weights[i], nxt, batch, l.fan_in, l.fan_out, aux=acts[i],
+                    act=prev.activation or "none", act_grad=True)
+            cur = nxt
+    # transactional update: check every tensor, then apply, then advance the counter
+    entries = []
+    for j, p in enumerate(params):
+        entries.append((p, lay.grads[j], lay.first[j] if has_first else None,
+                        lay.second[j] if lay.second else None, p.count))
+    common = {}
+    if kind == "sgd":
+        common = dict(lr=optimizer.learning_rate, momentum=optimizer.momentum,
+                      dampening=optimizer.dampening, weight_decay=optimizer.weight_decay,
+                      nesterov=optimizer.nesterov, has_momentum_slot=has_first)
+    else:
+        common = dict(lr=optimizer.learning_rate, beta1=optimizer.beta1, beta2=optimizer.beta2,
+                      eps=optimizer.epsilon, weight_decay=optimizer.weight_decay)
+    chunks = [entries[i:i + 24] for i in range(0, len(entries), 24)]
+    for phase in (0, 1):
+        for ch in chunks:
+            pb.optimizer(lay.counter, ch, kind=kind, phase=phase, **common)
+    pb.step_commit(lay.counter)
+    return pb, lay
+
+
+def lower_forward(spec: MlpSpec, batch: int):
+    """Inference program (Model.compute): inputs W_1..W_L, b_1..b_L, x; output prediction."""
+    pb = ProgramBuilder()
+    Ws = [pb.input(l.fan_in * l.fan_out) for l in spec.layers]
+    bs = [pb.input(l.fan_out) if l.bias else None for l in spec.layers]
+    x = pb.input(batch * spec.layers[0].fan_in)
+    out = pb.output(batch * spec.layers[-1].fan_out)
+    cur = x
+    for i, l in enumerate(spec.layers):
+        dst = out if i == len(spec.layers) - 1 else pb.internal(batch * l.fan_out)
+        pb.gemm(cur, Ws[i], dst, batch, l.fan_out, l.fan_in, trans_b=True, bias=bs[i],
+                act=l.activation)
+        cur = dst
+    return pb
+
+
+# ---- session ----
+@dataclass
+class TrainingStep:
+    objective: float
+    optimizer_step: int
+
+
+@dataclass
+class TrainingState:
+    """Byte-exact snapshot: parameters, first/second moment slots, completed steps."""
+    weights: list[np.ndarray]
+    biases: list[np.ndarray]
+    first: list[np.ndarray]
+    second: list[np.ndarray]
+    optimizer_steps: int
+
+
+class HipTrainingSession:
+    """A prepared, device-resident training step (TrainingSession analogue)."""
+
+    def __init__(self, ctx: HipContext, spec: MlpSpec, weights, biases, optimizer, batch: int,
+                 *, label_dtype: str = "i64"):
+        self.ctx = ctx
+        self.spec = spec
+        self.batch = batch
+        self.optimizer = optimizer
+        pb, lay = lower_training_step(spec, batch, optimizer, label_dtype=label_dtype)
+        self.layout = lay
+        self.label_dtype = label_dtype
+        self.program = HipProgram(ctx, pb.image())
+        self.W = [ctx.upload(np.asarray(w, np.float32)) for w in weights]
+        self.b = [ctx.upload(np.asarray(b, np.float32)) for b, l in zip(biases, spec.layers) if l.bias]
+        params = self.W + self.b
+        self.first = [ctx.upload(np.zeros(p.nbytes // 4, np.float32)) for p in params] if lay.first else []
+        self.second = [ctx.upload(np.zeros(p.nbytes // 4, np.float32)) for p in params] if lay.second else []
+        self.counter = ctx.upload(np.zeros(1, np.int64))
+        self.loss = ctx.buffer(4)
+        self._x = ctx.buffer(lay.x.nbytes)
+        self._y = ctx.buffer(lay.y.nbytes)
+
+    @classmethod
+    def open(cls, ctx, spec, weights, biases, optimizer, batch, **kw) -> "HipTrainingSession":
+        return cls(ctx, spec, weights, biases, optimizer, batch, **kw)
+
+    def _bindings(self, x: HipBuffer, y: HipBuffer):
+        return self.W + self.b + self.first + self.second + [self.counter, x, y]
+
+    def run_resident(self, x: HipBuffer, y: HipBuffer) -> None:
+        """One step on device-resident batch buffers; the objective stays on the device."""
+        self.program.run(self._bindings(x, y), [self.loss])
+
+    def run(self, x: np.ndarray, y: np.ndarray) -> TrainingStep:
+        """Uploads the batch (borrow), runs one step, downloads the objective."""
+        self._x.upload(np.ascontiguousarray(x, np.float32))
+        if self.spec.loss == "mse":
+            self._y.upload(np.ascontiguousarray(y, np.float32))
+        else:
+            self._y.upload(np.ascontiguousarray(y, np.int64 if self.label_dtype == "i64" else np.int32))
+        self.run_resident(self._x, self._y)
+        return TrainingStep(float(self.objective()), self.optimizer_steps)
+
+    def objective(self) -> np.float32:
+        return self.loss.download(np.float32, 1)[0]
+
+    @property
+    def optimizer_steps(self) -> int:
+        return int(self.counter.download(np.int64, 1)[0])
+
+    def state(self) -> TrainingState:
+        return TrainingState(
+            [w.download().reshape(l.fan_out, l.fan_in) for w, l in zip(self.W, self.spec.layers)],
+            [b.download() for b in self.b],
+            [m.download() for m in self.first],
+            [v.download() for v in self.second],
+            self.optimizer_steps)
+
+    def restore(self, st: TrainingState) -> None:
+        for buf, a in zip(self.W, st.weights):
+            buf.upload(np.asarray(a, np.float32))
+        for buf, a in zip(self.b, st.biases):
+            buf.upload(np.asarray(a, np.float32))
+        for buf, a in zip(self.first, st.first):
+            buf.upload(np.asarray(a, np.float32))
+        for buf, a in zip(self.second, st.second):
+            buf.upload(np.asarray(a, np.float32))
+        self.counter.upload(np.array([st.optimizer_steps], np.int64))
+
+    def close(self) -> None:
+        self.program.close()

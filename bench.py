@@ -40,6 +40,18 @@ def gemm_flops() -> float:
     return 2.0 * BATCH * WIDTH * WIDTH
 
 
+def measured_gemm_traffic():
+    """HBM bytes per 4096^3 GEMM launch from the committed rocprofv3 --pmc summary, or None."""
+    f = ROOT / "profiles" / "gemm_f32_mfma_4096_traffic.md"
+    try:
+        for line in f.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def build_session(ctx, seed=0):
     from synaptik_amd.training import HipTrainingSession, MlpSpec, Sgd, init_parameters
     spec = MlpSpec.chain([WIDTH] * (LAYERS + 1), hidden="relu", loss="mse")
@@ -83,13 +95,50 @@ def cpu_baseline(sample_batch: int, seed=0) -> dict:
     }
 
 
+def probe() -> int:
+    """Small fixed workload for rocprofv3 --pmc runs: FETCH_SIZE / WRITE_SIZE of the GEMM are
+    scaled by the same counters read for a plain copy kernel of known size."""
+    from synaptik_amd.native import HipContext, HipProgram
+    from synaptik_amd.program import ProgramBuilder
+    ctx = HipContext(0)
+    rng = np.random.default_rng(0)
+    pb = ProgramBuilder()
+    a = pb.input(BATCH * WIDTH)
+    w = pb.input(WIDTH * WIDTH)
+    c = pb.output(BATCH * WIDTH)
+    pb.gemm(a, w, c, BATCH, WIDTH, WIDTH, trans_b=True)
+    gemm = HipProgram(ctx, pb.image())
+    A = ctx.upload(rng.standard_normal(BATCH * WIDTH, dtype=np.float32))
+    W = ctx.upload(rng.standard_normal(WIDTH * WIDTH, dtype=np.float32))
+    C = ctx.buffer(BATCH * WIDTH * 4)
+    n_copy = 64 * 1024 * 1024  # 256 MiB read + 256 MiB written
+    pc = ProgramBuilder()
+    src = pc.input(n_copy)
+    dst = pc.output(n_copy)
+    pc.copy(src, dst, n_copy)
+    copy = HipProgram(ctx, pc.image())
+    S = ctx.upload(np.ones(n_copy, np.float32))
+    D = ctx.buffer(n_copy * 4)
+    for _ in range(3):
+        gemm.run([A, W], [C])
+        copy.run([S], [D])
+    print(json.dumps({"probe": "ok", "gemm_algorithmic_bytes": (2 * BATCH * WIDTH + WIDTH * WIDTH) * 4,
+                      "copy_bytes_each_way": n_copy * 4}), flush=True)
+    ctx.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-sample", type=int, default=16, help="rows for the CPU baseline (0 = skip)")
+    ap.add_argument("--probe", action="store_true",
+                    help="counter probe: 3 launches each of one 4096^3 NT GEMM and a 256 MiB copy")
     args = ap.parse_args()
+    if args.probe:
+        return probe()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this backend has no multi-GPU path "
               "(see the sharding note in DESIGN.md); run with --gpus 1", file=sys.stderr)
@@ -167,7 +216,7 @@ def main() -> int:
         "roofline": {"bound": "mfma", "kernel": "gemm_f32_mfma (14 per step, 4096^3 each)",
                      "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": measured_gemm_traffic()},
         "breakdown": breakdown,
         "cpu_baseline": cpu,
     }

@@ -23,6 +23,7 @@
 //     block of output tiles: tiles that share A row-panels and B column-panels share an L2.
 #include "common.h"
 #include "kernels.h"
+#include <algorithm>
 #include <type_traits>
 
 namespace shk {
@@ -215,6 +216,28 @@ gemm_f32_mfma(GemmParams p) {
   }
 }
 
+// K == 1: every output is exactly one product a*b (CpuMatmulReferenceKernel.java:34-119: a
+// singleton contraction is one typed product, no identity ADD), which keeps the sign of a zero
+// product; the MFMA path would add it to a +0 accumulator. Same epilogue as the MFMA kernel.
+__global__ void __launch_bounds__(256) gemm_k1_outer(GemmParams p) {
+  const int64_t total = p.M * p.N;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int64_t row = e / p.N, col = e - row * p.N;
+    const float a = p.A[row * (p.transA ? 1 : p.lda)];
+    const float b = p.B[col * (p.transB ? p.ldb : 1)];
+    float v = a * b;
+    if (p.mode == 0) {
+      if (p.bias != nullptr) v = v + p.bias[col];
+      v = apply_act(p.act, v);
+    } else {
+      v = act_grad(p.act, v, p.aux[row * p.ldaux + col]);
+    }
+    float* dst = p.C + row * p.ldc + col;
+    if (p.accumulate) v = *dst + v;
+    *dst = v;
+  }
+}
+
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
 hipError_t launch_cfg(const GemmParams& p, bool va, bool vb, hipStream_t s) {
   using S = GemmShape<BM, BN, BK, WM, WN>;
@@ -244,6 +267,12 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 
 hipError_t launch_gemm(const GemmParams& p, hipStream_t s) {
   if (p.M <= 0 || p.N <= 0) return hipSuccess;
+  if (p.K == 1) {
+    const int64_t total = p.M * p.N;
+    const unsigned blocks = (unsigned)std::min<int64_t>(65536, (total + 255) / 256);
+    hipLaunchKernelGGL(gemm_k1_outer, dim3(blocks), dim3(256), 0, s, p);
+    return hipGetLastError();
+  }
   // float4 loads need the contiguous extent, the leading dimension and the base aligned to 4.
   const int64_t a_contig = p.transA ? p.M : p.K;
   const int64_t b_contig = p.transB ? p.K : p.N;

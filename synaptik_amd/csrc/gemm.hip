@@ -24,6 +24,7 @@
 #include "common.h"
 #include "kernels.h"
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 namespace shk {
@@ -121,8 +122,9 @@ __device__ __forceinline__ void tile_of(int id, int tilesM, int tilesN, int& tm,
   tn = in_group / gsize;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VA, bool VB>
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VA, bool VB, int MINW = 1>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
+__attribute__((amdgpu_waves_per_eu(MINW)))
 gemm_f32_mfma(GemmParams p) {
   using S = GemmShape<BM, BN, BK, WM, WN>;
   constexpr int NT = S::NT, MI = S::MI, NI = S::NI, PA = S::PA, PB = S::PB;
@@ -166,20 +168,32 @@ gemm_f32_mfma(GemmParams p) {
       la.load(p.A, p.lda, m0, (int64_t)(kt + 1) * BK, p.M, p.K);
       lb.load(p.B, p.ldb, n0, (int64_t)(kt + 1) * BK, p.N, p.K);
     }
-    const float* a_s = As[cur] + wm * (MI * 32) + l32;
-    const float* b_s = Bs[cur] + wn * (NI * 32) + l32;
+    const float* a_s = As[cur] + wm * (MI * 32) + l32 + half * PA;
+    const float* b_s = Bs[cur] + wn * (NI * 32) + l32 + half * PB;
+    // Operand fragments are double-buffered in registers: the LDS reads for k-step s+1 are
+    // issued before the MFMAs of step s, so their latency hides behind the matrix pipe.
+    float a[2][MI], b[2][NI];
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 2) {
-      float a[MI], b[NI];
+    for (int i = 0; i < MI; ++i) a[0][i] = a_s[i * 32];
 #pragma unroll
-      for (int i = 0; i < MI; ++i) a[i] = a_s[(kk + half) * PA + i * 32];
+    for (int j = 0; j < NI; ++j) b[0][j] = b_s[j * 32];
 #pragma unroll
-      for (int j = 0; j < NI; ++j) b[j] = b_s[(kk + half) * PB + j * 32];
+    for (int st = 0; st < BK / 2; ++st) {
+      const int c = st & 1;
+      if (st + 1 < BK / 2) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i) a[c ^ 1][i] = a_s[(2 * st + 2) * PA + i * 32];
+#pragma unroll
+        for (int j = 0; j < NI; ++j) b[c ^ 1][j] = b_s[(2 * st + 2) * PB + j * 32];
+      }
+      // keep the next fragment's reads ahead of this step's MFMAs (the default scheduler sinks
+      // them below to save registers, which exposes the LDS latency again)
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NI; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c][i], b[c][j], acc[i][j], 0, 0, 0);
     }
     if (more) {
       la.store(As[cur ^ 1]);
@@ -238,26 +252,64 @@ __global__ void __launch_bounds__(256) gemm_k1_outer(GemmParams p) {
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB,
+          int MINW = (BM / WM) * (BN / WN) >= 8 ? 2 : 1>
 hipError_t launch_cfg(const GemmParams& p, bool va, bool vb, hipStream_t s) {
   using S = GemmShape<BM, BN, BK, WM, WN>;
   const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
   dim3 grid((unsigned)tiles), block(S::NT);
   if (va && vb)
-    hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, TA, TB, true, true>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, TA, TB, true, true, MINW>), grid, block, 0, s, p);
   else if (va)
-    hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, TA, TB, true, false>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, TA, TB, true, false, MINW>), grid, block, 0, s, p);
   else if (vb)
-    hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, TA, TB, false, true>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, TA, TB, false, true, MINW>), grid, block, 0, s, p);
   else
-    hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, TA, TB, false, false>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, TA, TB, false, false, MINW>), grid, block, 0, s, p);
   return hipGetLastError();
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int MINW>
+hipError_t launch_vec(const GemmParams& p, hipStream_t s) {
+  using S = GemmShape<BM, BN, BK, WM, WN>;
+  const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, TA, TB, true, true, MINW>), dim3((unsigned)tiles),
+                     dim3(S::NT), 0, s, p);
+  return hipGetLastError();
+}
+
+// Tile configuration override for tuning sweeps (SHK_HIP_GEMM_CONFIG, read once): applies to
+// large, fully vectorizable problems only; 0 keeps the default choice.
+int forced_config() {
+  static const int cfg = [] {
+    const char* e = getenv("SHK_HIP_GEMM_CONFIG");
+    return e ? atoi(e) : 0;
+  }();
+  return cfg;
 }
 
 template <bool TA, bool TB>
 hipError_t launch_layout(const GemmParams& p, bool va, bool vb, hipStream_t s) {
   const int64_t big_tiles = ((p.M + 127) / 128) * ((p.N + 127) / 128);
-  if (big_tiles >= 512) return launch_cfg<128, 128, 16, 64, 64, TA, TB>(p, va, vb, s);
+  if (va && vb && big_tiles >= 512) {
+    switch (forced_config()) {
+      case 1: return launch_vec<128, 128, 16, 64, 64, TA, TB, 4>(p, s);
+      case 2: return launch_vec<256, 128, 16, 64, 64, TA, TB, 2>(p, s);
+      case 3: return launch_vec<256, 256, 16, 128, 64, TA, TB, 2>(p, s);
+      case 4: return launch_vec<128, 128, 32, 64, 64, TA, TB, 1>(p, s);
+      case 5: return launch_vec<256, 128, 16, 128, 64, TA, TB, 1>(p, s);
+      case 6: return launch_vec<128, 256, 16, 64, 128, TA, TB, 1>(p, s);
+      case 7: return launch_vec<256, 256, 16, 64, 64, TA, TB, 1>(p, s);
+      case 8: return launch_vec<256, 128, 32, 64, 64, TA, TB, 2>(p, s);
+      case 9: return launch_vec<128, 256, 16, 64, 64, TA, TB, 2>(p, s);
+      default: break;
+    }
+  }
+  // Default: 256x128 tiles of 8 waves (each 64x64) while they still give every CU a tile;
+  // 128x128 x 4 waves for mid-size problems; 64x64 x 4 waves for small ones.
+  const int64_t wide_tiles = ((p.M + 255) / 256) * ((p.N + 127) / 128);
+  if (wide_tiles >= 256) return launch_cfg<256, 128, 16, 64, 64, TA, TB>(p, va, vb, s);
+  if (big_tiles >= 256) return launch_cfg<128, 128, 16, 64, 64, TA, TB>(p, va, vb, s);
   return launch_cfg<64, 64, 16, 32, 32, TA, TB>(p, va, vb, s);
 }
 

@@ -128,12 +128,91 @@ def probe() -> int:
     return 0
 
 
+def secondary(ctx, reps: int = 5) -> dict:
+    """The other BASELINE configs, measured on the same context (not the headline value)."""
+    from synaptik_amd.native import HipProgram
+    from synaptik_amd.program import ProgramBuilder
+    from synaptik_amd.training import (Adam, HipTrainingSession, MlpSpec, init_parameters,
+                                       lower_dense_layer)
+    out = {}
+    rng = np.random.default_rng(7)
+    # C5: softmax + LSE + mean forward, softmax-with-LSE-cotangent backward over [65536, 4096]
+    R, C = 65536, 4096
+    pb = ProgramBuilder()
+    sx, sdp = pb.input(R * C), pb.input(R * C)
+    sp, sl, sm, sdx = pb.output(R * C), pb.output(R), pb.output(1), pb.output(R * C)
+    pb.softmax(sx, sp, R, C, lse=sl)
+    pb.reduce_all(sl, sm, R, "mean")
+    pb.softmax_bwd(sp, sdp, sdx, R, C, rowscale_const=1.0 / R)
+    prog = HipProgram(ctx, pb.image())
+    x = rng.standard_normal((R, C), dtype=np.float32) * 2
+    mask = rng.random((R, C), dtype=np.float32) < 0.01
+    x[mask] = 30.0
+    bx, bdp = ctx.upload(x), ctx.upload(rng.standard_normal((R, C), dtype=np.float32))
+    del x, mask
+    bp, bl, bm, bdx = ctx.buffer(R * C * 4), ctx.buffer(R * 4), ctx.buffer(4), ctx.buffer(R * C * 4)
+    prog.run([bx, bdp], [bp, bl, bm, bdx])
+    prog.set_profiling(True)
+    for _ in range(reps):
+        prog.run([bx, bdp], [bp, bl, bm, bdx])
+    t, runs = prog.step_times()
+    fwd_ms, mean_ms, bwd_ms = (v / runs for v in t)
+    fwd_bytes = R * C * 8 + R * 4
+    bwd_bytes = R * C * 12
+    out["c5_softmax_stress"] = {
+        "shape": [R, C], "fwd_ms": round(fwd_ms, 4), "mean_ms": round(mean_ms, 4), "bwd_ms": round(bwd_ms, 4),
+        "fwd_GBps": round(fwd_bytes / fwd_ms / 1e6, 1), "bwd_GBps": round(bwd_bytes / bwd_ms / 1e6, 1),
+        "fwd_frac_hbm": round(fwd_bytes / fwd_ms / 1e6 / HBM_PEAK_GBS, 4),
+        "bwd_frac_hbm": round(bwd_bytes / bwd_ms / 1e6 / HBM_PEAK_GBS, 4)}
+    prog.close()
+    for b in (bx, bdp, bp, bdx):
+        b.close()
+    # C2: single fused layer forward + backward, X [8192,1024] . W [1024,1024]
+    B, I, O = 8192, 1024, 1024
+    pb, outs = lower_dense_layer(B, I, O, "relu", "in_out")
+    prog = HipProgram(ctx, pb.image())
+    ins = [ctx.upload(rng.standard_normal(n, dtype=np.float32)) for n in (B * I, I * O, O, B * O)]
+    obs = [ctx.buffer(s.nbytes) for s in outs]
+    prog.run(ins, obs)
+    prog.set_profiling(True)
+    t0 = time.perf_counter()
+    for _ in range(reps * 4):
+        prog.run(ins, obs)
+    wall = (time.perf_counter() - t0) / (reps * 4) * 1e3
+    t, runs = prog.step_times()
+    dev = sum(t) / runs
+    out["c2_fused_layer"] = {"ms": round(wall, 4), "device_ms": round(dev, 4),
+                             "TFLOPs": round(3 * 2 * B * I * O / dev / 1e9, 1)}
+    prog.close()
+    # C3: 784 -> 1024 -> 1024 -> 10 classifier, softmax-CE, Adam, batch 1024, 50 steps
+    spec = MlpSpec.chain([784, 1024, 1024, 10], hidden="relu", loss="ce")
+    Ws, bs = init_parameters(spec, 0, "he_normal")
+    sess = HipTrainingSession.open(ctx, spec, Ws, bs, Adam(1e-3, 0.9, 0.999, 1e-8), 1024)
+    xb = ctx.upload(rng.uniform(0, 1, (1024, 784)).astype(np.float32))
+    yb = ctx.upload(rng.integers(0, 10, 1024).astype(np.int64))
+    first = None
+    for i in range(5):
+        sess.run_resident(xb, yb)
+    t0 = time.perf_counter()
+    for i in range(50):
+        sess.run_resident(xb, yb)
+        if i == 0:
+            first = float(sess.objective())
+    wall = time.perf_counter() - t0
+    out["c3_classifier_adam"] = {"samples_per_s": round(50 * 1024 / wall, 1),
+                                 "ms_per_step": round(wall / 50 * 1e3, 4),
+                                 "objective_first": first, "objective_last": float(sess.objective())}
+    sess.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-sample", type=int, default=16, help="rows for the CPU baseline (0 = skip)")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the C2/C3/C5 lines")
     ap.add_argument("--probe", action="store_true",
                     help="counter probe: 3 launches each of one 4096^3 NT GEMM and a 256 MiB copy")
     args = ap.parse_args()
@@ -191,6 +270,10 @@ def main() -> int:
     opt_gbs = (32.0 * n_params) / (opt_ms * 1e-3) / 1e9 if opt_ms > 0 else None
     print(f"[bench] breakdown {breakdown}; optimizer {opt_gbs:.0f} GB/s", file=sys.stderr, flush=True)
 
+    sess.close()
+    extra = None if args.no_secondary else secondary(ctx)
+    if extra:
+        print(f"[bench] secondary {extra}", file=sys.stderr, flush=True)
     cpu = None
     if args.cpu_sample > 0:
         cpu = cpu_baseline(args.cpu_sample)
@@ -219,9 +302,9 @@ def main() -> int:
                      "traffic": measured_gemm_traffic()},
         "breakdown": breakdown,
         "cpu_baseline": cpu,
+        "secondary": extra,
     }
     print(json.dumps(result), flush=True)
-    sess.close()
     ctx.close()
     return 0
 

@@ -110,7 +110,8 @@ struct OptParams {
   OptTensor t[OPT_MAX_TENSORS];
   int count;
   int64_t total;
-  int kind;        // 0 SGD, 1 Adam (coupled decay), 2 AdamW (decoupled decay)
+  int kind;        // 0 SGD, 1 Adam (coupled decay), 2 AdamW (decoupled decay),
+                   // 3 accumulate-sum, 4 commit accumulator, 5 clear accumulator (gated)
   int phase;       // 0 check (validate every intermediate), 1 apply (commit if status clear)
   float lr, momentum, dampening, weight_decay;  // SGD
   int nesterov, has_momentum_slot;

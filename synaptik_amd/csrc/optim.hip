@@ -134,12 +134,44 @@ __device__ __forceinline__ bool adam_element(const OptParams& p, const Coeffs& k
   return ok;
 }
 
+// Gradient accumulation (TrainingParameter.stageAccumulation:374-389, GradientMode):
+//   kind 3  p = m + g with every candidate checked finite (m: accumulator, p: the step's
+//           gradient buffer, rewritten in place);
+//   kind 4  m = g, only if the status word is clear (commit of an ACCUMULATE run);
+//   kind 5  m = 0, only if the status word is clear (accumulator emptied by a successful step).
+__device__ void accumulation_block(const OptParams& p, const OptTensor& T, int64_t base) {
+  if (p.kind != 3 && *(volatile const uint32_t*)p.status != 0u) return;
+  bool ok = true;
+#pragma unroll
+  for (int q = 0; q < OPT_PER_THREAD; ++q) {
+    const int64_t i = base + q * OPT_NT + threadIdx.x;
+    if (i >= T.n) break;
+    if (p.kind == 3) {
+      const float c = T.m[i] + T.g[i];
+      ok &= is_finite(c);
+      T.p[i] = c;
+    } else if (p.kind == 4) {
+      T.m[i] = T.g[i];
+    } else {
+      T.m[i] = 0.0f;
+    }
+  }
+  if (p.kind == 3) {
+    const int bad = wave_or(ok ? 0 : 1);
+    if (bad && (threadIdx.x & 63) == 0) atomicOr(p.status, (uint32_t)DEV_NON_FINITE);
+  }
+}
+
 __global__ void __launch_bounds__(OPT_NT) optimizer_kernel(OptParams p) {
   // Tensor of this block: the table holds each tensor's first block index in `start`.
   int t = 0;
   for (int i = 1; i < p.count; ++i)
     if ((int64_t)blockIdx.x >= p.t[i].start) t = i;
   const OptTensor T = p.t[t];
+  if (p.kind >= 3) {
+    accumulation_block(p, T, ((int64_t)blockIdx.x - T.start) * OPT_CHUNK);
+    return;
+  }
   if (p.phase == 1 && *(volatile const uint32_t*)p.status != 0u) return;
   const int64_t completed = *p.completed_steps;
   const bool first = completed == 0;

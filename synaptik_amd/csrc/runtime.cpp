@@ -360,7 +360,7 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
     }
     case OP_OPTIMIZER: {
       const int64_t kind = a[0], phase = a[1];
-      if (kind < 0 || kind > 2 || (phase != 0 && phase != 1))
+      if (kind < 0 || kind > 5 || (phase != 0 && phase != 1))
         return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: invalid optimizer", idx);
       if (!v.slot_ok(s[0], false, "step counter") || !v.holds(s[0], 1, DT_I64, "step counter"))
         return v.err;
@@ -369,9 +369,10 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
         return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: bad optimizer tensor table", idx);
       const OptEntry* e = reinterpret_cast<const OptEntry*>(st.payload.data());
       for (size_t i = 0; i < n; ++i) {
-        const bool adam = kind != 0;
+        const bool adam = kind == 1 || kind == 2;
+        const bool needs_m = adam || kind >= 3;  // accumulation kinds use m as the accumulator
         if (!v.slot_ok(e[i].p, false, "param") || !v.slot_ok(e[i].g, false, "grad") ||
-            !v.slot_ok(e[i].m, !adam, "momentum") || !v.slot_ok(e[i].v, !adam, "second moment") ||
+            !v.slot_ok(e[i].m, !needs_m, "momentum") || !v.slot_ok(e[i].v, !adam, "second moment") ||
             !v.holds(e[i].p, e[i].n, DT_F32, "param") || !v.holds(e[i].g, e[i].n, DT_F32, "grad") ||
             !v.holds(e[i].m, e[i].n, DT_F32, "momentum") || !v.holds(e[i].v, e[i].n, DT_F32, "second moment") ||
             !v.writable(e[i].p, "param") || !v.writable(e[i].m, "momentum") || !v.writable(e[i].v, "second moment"))

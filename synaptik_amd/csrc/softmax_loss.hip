@@ -17,6 +17,9 @@ namespace shk {
 namespace {
 
 constexpr int SM_NT = 256;
+#ifndef SHK_SOFTMAX_EXP
+#define SHK_SOFTMAX_EXP(v) ((float)exp((double)(v)))
+#endif
 
 __device__ __forceinline__ int block_or(int v, int* lds) {
   v = wave_or(v);
@@ -36,7 +39,7 @@ struct RowStats {
 };
 
 __device__ __forceinline__ float shifted_exp(float x, float shift) {
-  return (float)exp((double)(x - shift));
+  return SHK_SOFTMAX_EXP(x - shift);
 }
 
 // V float4 per thread in registers (C <= V * 4 * SM_NT, C % 4 == 0).
@@ -84,15 +87,19 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restric
     return;
   }
   const float shift = (neg_inf && m == m) ? 0.0f : m;
+  // One binary64 exponential per element: softmax keeps the rounded addends in registers and
+  // divides them by the sum; log-softmax only needs the sum and recomputes x - shift.
+  float4 e[V];
   double s = 0.0;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int c = threadIdx.x + i * SM_NT;
     if (c < C4) {
-      s += (double)shifted_exp(v[i].x, shift);
-      s += (double)shifted_exp(v[i].y, shift);
-      s += (double)shifted_exp(v[i].z, shift);
-      s += (double)shifted_exp(v[i].w, shift);
+      e[i].x = shifted_exp(v[i].x, shift);
+      e[i].y = shifted_exp(v[i].y, shift);
+      e[i].z = shifted_exp(v[i].z, shift);
+      e[i].w = shifted_exp(v[i].w, shift);
+      s += ((double)e[i].x + (double)e[i].y) + ((double)e[i].z + (double)e[i].w);
     }
   }
   const float sum = (float)block_sum<SM_NT>(s, dl);
@@ -108,10 +115,10 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restric
         o.z = (v[i].z - shift) - logsum;
         o.w = (v[i].w - shift) - logsum;
       } else {
-        o.x = shifted_exp(v[i].x, shift) / sum;
-        o.y = shifted_exp(v[i].y, shift) / sum;
-        o.z = shifted_exp(v[i].z, shift) / sum;
-        o.w = shifted_exp(v[i].w, shift) / sum;
+        o.x = e[i].x / sum;
+        o.y = e[i].y / sum;
+        o.z = e[i].z / sum;
+        o.w = e[i].w / sum;
       }
       yr[c] = o;
     }

@@ -184,7 +184,7 @@ class ProgramBuilder:
                   dampening=0.0, weight_decay=0.0, nesterov=False, has_momentum_slot=False,
                   beta1=0.9, beta2=0.999, eps=1e-8) -> Step:
         """tensors: list of (param, grad, m, v, count) slots (m/v None where absent)."""
-        k = {"sgd": 0, "adam": 1, "adamw": 2}[kind]
+        k = {"sgd": 0, "adam": 1, "adamw": 2, "acc_sum": 3, "acc_commit": 4, "acc_clear": 5}[kind]
         payload = b"".join(struct.pack("<iiiiq", _sid(p), _sid(g), _sid(m), _sid(v), int(n))
                            for (p, g, m, v, n) in tensors)
         return self._add(OP_OPTIMIZER, [counter], [k, phase, int(nesterov), int(has_momentum_slot)],

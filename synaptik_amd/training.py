@@ -29,6 +29,16 @@ from .program import ProgramBuilder, Slot
 ACTIVATIONS = (None, "relu", "tanh", "sigmoid")
 
 
+class GradientMode:
+    """How one successful run uses its gradients (GradientMode.java):
+    RESET_AND_STEP ignores and empties the pending accumulator and steps from this run;
+    ACCUMULATE adds this run's gradients to the accumulator without stepping;
+    ACCUMULATE_AND_STEP adds them, steps from the complete sum and empties the accumulator."""
+    RESET_AND_STEP = "reset_and_step"
+    ACCUMULATE = "accumulate"
+    ACCUMULATE_AND_STEP = "accumulate_and_step"
+
+
 # ---- optimizer configurations (immutable, validated like the reference records) ----
 @dataclass(frozen=True)
 class Sgd:
@@ -154,6 +164,7 @@ class TrainingLayout:
     biases: list[Slot] = field(default_factory=list)
     first: list[Slot] = field(default_factory=list)    # momentum / first-moment slots
     second: list[Slot] = field(default_factory=list)   # second-moment slots (Adam)
+    accum: list[Slot] = field(default_factory=list)    # gradient accumulators (accumulating modes)
     counter: Slot | None = None
     x: Slot | None = None
     y: Slot | None = None
@@ -169,13 +180,18 @@ def _optimizer_kind(opt) -> str:
     raise TypeError(f"unsupported optimizer {opt!r}")
 
 
-def lower_training_step(spec: MlpSpec, batch: int, optimizer, *, label_dtype: str = "i64"):
+def lower_training_step(spec: MlpSpec, batch: int, optimizer, *, label_dtype: str = "i64",
+                        mode: str = GradientMode.RESET_AND_STEP, clear_accumulator: bool = False):
     """Lowers one training step of `spec` at `batch` rows to a program image.
 
     Inputs (in order): W_1..W_L, b_1..b_L (INOUT), first-moment slots per tensor (INOUT, SGD
-    with momentum and Adam), second-moment slots (INOUT, Adam), completed-step counter (INOUT,
+    with momentum and Adam), second-moment slots (INOUT, Adam), gradient accumulators (INOUT,
+    accumulating modes and RESET_AND_STEP with clear_accumulator), completed-step counter (INOUT,
     int64), x [batch, in], y ([batch, out] f32 for MSE; [batch] int for CE).
     Output: objective [1].
+
+    Every mode is transactional: a non-finite accumulated candidate or optimizer intermediate
+    leaves parameters, slots, accumulators and the counter unchanged.
     """
     kind = _optimizer_kind(optimizer)
     pb = ProgramBuilder()
@@ -191,6 +207,9 @@ def lower_training_step(spec: MlpSpec, batch: int, optimizer, *, label_dtype: st
         lay.first = [pb.input(p.count, inout=True) for p in params]
     if kind != "sgd":
         lay.second = [pb.input(p.count, inout=True) for p in params]
+    uses_acc = mode != GradientMode.RESET_AND_STEP or clear_accumulator
+    if uses_acc:
+        lay.accum = [pb.input(p.count, inout=True) for p in params]
     lay.counter = pb.input(1, "i64", inout=True)
     lay.x = pb.input(batch * spec.layers[0].fan_in)
     out_w = spec.layers[-1].fan_out
@@ -236,6 +255,15 @@ def lower_training_step(spec: MlpSpec, batch: int, optimizer, *, label_dtype: st
             pb.gemm(cur, lay.weights[i], nxt, batch, l.fan_in, l.fan_out, aux=acts[i],
                     act=prev.activation or "none", act_grad=True)
             cur = nxt
+    if mode != GradientMode.RESET_AND_STEP:
+        # G = accumulator + G for every tensor, each candidate checked finite
+        acc_entries = [(g, g, a, None, g.count) for g, a in zip(lay.grads, lay.accum)]
+        for i in range(0, len(acc_entries), 24):
+            pb.optimizer(lay.counter, acc_entries[i:i + 24], kind="acc_sum", phase=0, lr=0.0)
+        if mode == GradientMode.ACCUMULATE:
+            for i in range(0, len(acc_entries), 24):
+                pb.optimizer(lay.counter, acc_entries[i:i + 24], kind="acc_commit", phase=1, lr=0.0)
+            return pb, lay
     # transactional update: check every tensor, then apply, then advance the counter
     entries = []
     for j, p in enumerate(params):
@@ -253,6 +281,10 @@ def lower_training_step(spec: MlpSpec, batch: int, optimizer, *, label_dtype: st
     for phase in (0, 1):
         for ch in chunks:
             pb.optimizer(lay.counter, ch, kind=kind, phase=phase, **common)
+    if uses_acc:
+        acc_entries = [(g, g, a, None, g.count) for g, a in zip(lay.grads, lay.accum)]
+        for i in range(0, len(acc_entries), 24):
+            pb.optimizer(lay.counter, acc_entries[i:i + 24], kind="acc_clear", phase=1, lr=0.0)
     pb.step_commit(lay.counter)
     return pb, lay
 
@@ -277,17 +309,20 @@ def lower_forward(spec: MlpSpec, batch: int):
 @dataclass
 class TrainingStep:
     objective: float
-    optimizer_step: int
+    optimizer_step: int | None
+    accumulated_gradient_runs: int = 0
 
 
 @dataclass
 class TrainingState:
-    """Byte-exact snapshot: parameters, first/second moment slots, completed steps."""
+    """Byte-exact snapshot: parameters, first/second moment slots, accumulators, counters."""
     weights: list[np.ndarray]
     biases: list[np.ndarray]
     first: list[np.ndarray]
     second: list[np.ndarray]
     optimizer_steps: int
+    accumulators: list[np.ndarray] = field(default_factory=list)
+    accumulated_gradient_runs: int = 0
 
 
 class HipTrainingSession:
@@ -299,15 +334,17 @@ class HipTrainingSession:
         self.spec = spec
         self.batch = batch
         self.optimizer = optimizer
-        pb, lay = lower_training_step(spec, batch, optimizer, label_dtype=label_dtype)
-        self.layout = lay
         self.label_dtype = label_dtype
-        self.program = HipProgram(ctx, pb.image())
+        self._programs: dict[tuple, tuple[HipProgram, TrainingLayout]] = {}
+        self.program, lay = self._program(GradientMode.RESET_AND_STEP, False)
+        self.layout = lay
         self.W = [ctx.upload(np.asarray(w, np.float32)) for w in weights]
         self.b = [ctx.upload(np.asarray(b, np.float32)) for b, l in zip(biases, spec.layers) if l.bias]
         params = self.W + self.b
         self.first = [ctx.upload(np.zeros(p.nbytes // 4, np.float32)) for p in params] if lay.first else []
         self.second = [ctx.upload(np.zeros(p.nbytes // 4, np.float32)) for p in params] if lay.second else []
+        self.accum: list[HipBuffer] = []
+        self.accumulated_gradient_runs = 0
         self.counter = ctx.upload(np.zeros(1, np.int64))
         self.loss = ctx.buffer(4)
         self._x = ctx.buffer(lay.x.nbytes)
@@ -317,22 +354,54 @@ class HipTrainingSession:
     def open(cls, ctx, spec, weights, biases, optimizer, batch, **kw) -> "HipTrainingSession":
         return cls(ctx, spec, weights, biases, optimizer, batch, **kw)
 
-    def _bindings(self, x: HipBuffer, y: HipBuffer):
-        return self.W + self.b + self.first + self.second + [self.counter, x, y]
+    def _program(self, mode: str, clear: bool):
+        key = (mode, clear)
+        if key not in self._programs:
+            pb, lay = lower_training_step(self.spec, self.batch, self.optimizer,
+                                          label_dtype=self.label_dtype, mode=mode,
+                                          clear_accumulator=clear)
+            self._programs[key] = (HipProgram(self.ctx, pb.image()), lay)
+        return self._programs[key]
 
-    def run_resident(self, x: HipBuffer, y: HipBuffer) -> None:
-        """One step on device-resident batch buffers; the objective stays on the device."""
-        self.program.run(self._bindings(x, y), [self.loss])
+    def _ensure_accumulators(self):
+        if not self.accum:
+            self.accum = [self.ctx.upload(np.zeros(p.nbytes // 4, np.float32)) for p in self.W + self.b]
 
-    def run(self, x: np.ndarray, y: np.ndarray) -> TrainingStep:
-        """Uploads the batch (borrow), runs one step, downloads the objective."""
+    def run_resident(self, x: HipBuffer, y: HipBuffer,
+                     mode: str = GradientMode.RESET_AND_STEP) -> None:
+        """One run on device-resident batch buffers; the objective stays on the device."""
+        pending = self.accumulated_gradient_runs > 0
+        if mode == GradientMode.RESET_AND_STEP and not pending:
+            prog, _ = self._programs[(mode, False)]
+            prog.run(self.W + self.b + self.first + self.second + [self.counter, x, y], [self.loss])
+            return
+        self._ensure_accumulators()
+        prog, _ = self._program(mode, mode == GradientMode.RESET_AND_STEP)
+        prog.run(self.W + self.b + self.first + self.second + self.accum + [self.counter, x, y],
+                 [self.loss])
+        # reached only when the program committed
+        if mode == GradientMode.ACCUMULATE:
+            self.accumulated_gradient_runs += 1
+        else:
+            self.accumulated_gradient_runs = 0
+
+    def run(self, x: np.ndarray, y: np.ndarray,
+            mode: str = GradientMode.RESET_AND_STEP) -> TrainingStep:
+        """Uploads the batch (borrow), runs once in `mode`, downloads the objective."""
         self._x.upload(np.ascontiguousarray(x, np.float32))
         if self.spec.loss == "mse":
             self._y.upload(np.ascontiguousarray(y, np.float32))
         else:
             self._y.upload(np.ascontiguousarray(y, np.int64 if self.label_dtype == "i64" else np.int32))
-        self.run_resident(self._x, self._y)
-        return TrainingStep(float(self.objective()), self.optimizer_steps)
+        self.run_resident(self._x, self._y, mode)
+        step = None if mode == GradientMode.ACCUMULATE else self.optimizer_steps
+        return TrainingStep(float(self.objective()), step, self.accumulated_gradient_runs)
+
+    def zero_grad(self) -> None:
+        """Empties the pending gradient accumulator (TrainingSession.zeroGrad)."""
+        for a in self.accum:
+            a.upload(np.zeros(a.nbytes // 4, np.float32))
+        self.accumulated_gradient_runs = 0
 
     def objective(self) -> np.float32:
         return self.loss.download(np.float32, 1)[0]
@@ -347,7 +416,9 @@ class HipTrainingSession:
             [b.download() for b in self.b],
             [m.download() for m in self.first],
             [v.download() for v in self.second],
-            self.optimizer_steps)
+            self.optimizer_steps,
+            [a.download() for a in self.accum] if self.accumulated_gradient_runs else [],
+            self.accumulated_gradient_runs)
 
     def restore(self, st: TrainingState) -> None:
         for buf, a in zip(self.W, st.weights):
@@ -359,9 +430,18 @@ class HipTrainingSession:
         for buf, a in zip(self.second, st.second):
             buf.upload(np.asarray(a, np.float32))
         self.counter.upload(np.array([st.optimizer_steps], np.int64))
+        if st.accumulated_gradient_runs:
+            self._ensure_accumulators()
+            for buf, a in zip(self.accum, st.accumulators):
+                buf.upload(np.asarray(a, np.float32))
+        else:
+            self.zero_grad()
+        self.accumulated_gradient_runs = st.accumulated_gradient_runs
 
     def close(self) -> None:
-        self.program.close()
+        for prog, _ in self._programs.values():
+            prog.close()
+        self._programs.clear()
 
 
 def lower_dense_layer(batch: int, fan_in: int, fan_out: int, activation: str | None = "relu",

@@ -236,6 +236,25 @@ __global__ void __launch_bounds__(256) reduce_all_pass2(const double* part, int 
   if (threadIdx.x == 0) out[0] = kind == 1 ? (float)(s / (double)n) : (float)s;
 }
 
+// Rank-2 transpose (PERMUTE [1,0] materialized): 32x32 tiles staged through LDS (padded pitch)
+// so both the read of X and the write of Y are coalesced.
+__global__ void __launch_bounds__(256) transpose_kernel(const float* __restrict__ x,
+                                                        float* __restrict__ y, int64_t R,
+                                                        int64_t C) {
+  __shared__ float tile[32][33];
+  const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = r0 + k, c = c0 + tx;
+    if (r < R && c < C) tile[k][tx] = x[r * C + c];
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t c = c0 + k, r = r0 + tx;
+    if (r < R && c < C) y[c * R + r] = tile[tx][k];
+  }
+}
+
 unsigned grid_for(int64_t n, int per_thread, int nt = 256) {
   int64_t g = (n + (int64_t)nt * per_thread - 1) / ((int64_t)nt * per_thread);
   if (g < 1) g = 1;
@@ -249,6 +268,13 @@ hipError_t launch_pointwise(const PwParams& p, hipStream_t s) {
   const int64_t n = p.R * p.C;
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(pointwise_kernel, dim3(grid_for(n, 4)), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_transpose(const float* x, float* y, int64_t R, int64_t C, hipStream_t s) {
+  if (R <= 0 || C <= 0) return hipSuccess;
+  dim3 g((unsigned)((C + 31) / 32), (unsigned)((R + 31) / 32));
+  hipLaunchKernelGGL(transpose_kernel, g, dim3(256), 0, s, x, y, R, C);
   return hipGetLastError();
 }
 

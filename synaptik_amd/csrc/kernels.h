@@ -126,5 +126,7 @@ hipError_t launch_step_commit(int64_t* counter, const uint32_t* status, hipStrea
 hipError_t launch_fill(float* x, int64_t n, float value, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* x, int64_t n, uint32_t value, hipStream_t s);
 hipError_t launch_copy(const float* src, float* dst, int64_t n, hipStream_t s);
+// Y[C,R] = X[R,C]^T
+hipError_t launch_transpose(const float* x, float* y, int64_t R, int64_t C, hipStream_t s);
 
 }  // namespace shk

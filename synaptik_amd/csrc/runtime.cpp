@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -50,13 +51,28 @@ constexpr uint32_t kProgramMagic = 0x50484B53u;
 constexpr uint32_t kImageMagic = 0x504B4853u;    // "SHKP" little-endian
 constexpr uint32_t kImageVersion = 1u;
 
+// A context stays alive while any buffer or program created from it is alive: the owner's
+// release drops one reference, every child holds one, and the last release destroys it. A child
+// released after its owner therefore never touches freed memory.
 struct Context {
   uint32_t magic = kContextMagic;
   int device = 0;
   hipStream_t stream = nullptr;
   uint32_t* host_status = nullptr;  // pinned
   std::mutex mutex;
+  std::atomic<int64_t> refs{1};
+  std::atomic<bool> released{false};
 };
+
+void context_unref(Context* c) {
+  if (c->refs.fetch_sub(1) != 1) return;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  (void)hipStreamDestroy(c->stream);
+  (void)hipHostFree(c->host_status);
+  c->magic = 0;
+  delete c;
+}
 
 struct Buffer {
   uint32_t magic = kBufferMagic;
@@ -84,6 +100,7 @@ enum Opcode : uint32_t {
   OP_STEP_COMMIT = 12,
   OP_FILL = 13,
   OP_COPY = 14,
+  OP_TRANSPOSE = 15,
 };
 
 #pragma pack(push, 1)
@@ -138,6 +155,12 @@ T* checked(void* h) {
   if (h == nullptr) return nullptr;
   T* t = static_cast<T*>(h);
   return t->magic == M ? t : nullptr;
+}
+
+// A context handle the owner has not released yet.
+Context* live_context(void* h) {
+  Context* c = checked<Context, kContextMagic>(h);
+  return (c != nullptr && !c->released.load()) ? c : nullptr;
 }
 
 uint64_t dtype_size(uint32_t dt) {
@@ -397,6 +420,14 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
           !v.writable(s[1], "dst"))
         return v.err;
       return SHK_HIP_STATUS_OK;
+    case OP_TRANSPOSE:
+      if (a[0] < 0 || a[1] < 0 || a[0] > INT32_MAX / 2 || a[1] > INT32_MAX / 2)
+        return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid transpose", idx);
+      if (!v.slot_ok(s[0], false, "X") || !v.slot_ok(s[1], false, "Y") ||
+          !v.holds(s[0], a[0] * a[1], DT_F32, "X") || !v.holds(s[1], a[0] * a[1], DT_F32, "Y") ||
+          !v.writable(s[1], "Y"))
+        return v.err;
+      return SHK_HIP_STATUS_OK;
     default:
       return fail(SHK_HIP_STATUS_UNSUPPORTED_OPERATION, "step %zu: unknown opcode %u", idx, r.opcode);
   }
@@ -487,6 +518,8 @@ hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipSt
       return shk::launch_fill(b.get<float>(s[0]), a[0], r.farg[0], stream);
     case OP_COPY:
       return shk::launch_copy(b.get<const float>(s[0]), b.get<float>(s[1]), a[0], stream);
+    case OP_TRANSPOSE:
+      return shk::launch_transpose(b.get<const float>(s[0]), b.get<float>(s[1]), a[0], a[1], stream);
     default:
       return hipErrorInvalidValue;
   }
@@ -497,7 +530,9 @@ void destroy_program(Program* p) {
   for (hipEvent_t e : p->events) (void)hipEventDestroy(e);
   if (p->arena != nullptr) (void)hipFree(p->arena);
   p->magic = 0;
+  Context* c = p->ctx;
   delete p;
+  if (c != nullptr) context_unref(c);
 }
 
 }  // namespace
@@ -545,20 +580,16 @@ int32_t shk_hip_context_create(int32_t device_ordinal, void** out_context) {
 }
 
 int32_t shk_hip_context_release(void* context) {
-  Context* c = checked<Context, kContextMagic>(context);
-  if (c == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a context handle");
-  (void)hipSetDevice(c->device);
-  (void)hipStreamSynchronize(c->stream);
-  (void)hipStreamDestroy(c->stream);
-  (void)hipHostFree(c->host_status);
-  c->magic = 0;
-  delete c;
+  Context* c = live_context(context);
+  if (c == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a live context handle");
+  if (c->released.exchange(true)) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "context already released");
+  context_unref(c);
   return SHK_HIP_STATUS_OK;
 }
 
 int32_t shk_hip_device_info(void* context, int32_t* out_compute_units, int32_t* out_clock_khz,
                             uint64_t* out_memory_bytes, char* out_name, uint64_t name_capacity) {
-  Context* c = checked<Context, kContextMagic>(context);
+  Context* c = live_context(context);
   if (c == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a context handle");
   hipDeviceProp_t prop;
   HIP_TRY(hipGetDeviceProperties(&prop, c->device));
@@ -576,8 +607,8 @@ int32_t shk_hip_device_info(void* context, int32_t* out_compute_units, int32_t* 
 int32_t shk_hip_buffer_create(void* context, uint64_t byte_size, void** out_buffer) {
   if (out_buffer == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "out_buffer is null");
   *out_buffer = nullptr;
-  Context* c = checked<Context, kContextMagic>(context);
-  if (c == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a context handle");
+  Context* c = live_context(context);
+  if (c == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a live context handle");
   try {
     HIP_TRY(hipSetDevice(c->device));
     void* p = nullptr;
@@ -588,6 +619,7 @@ int32_t shk_hip_buffer_create(void* context, uint64_t byte_size, void** out_buff
     b->ctx = c;
     b->ptr = p;
     b->bytes = byte_size;
+    c->refs.fetch_add(1);
     *out_buffer = b;
     return SHK_HIP_STATUS_OK;
   } catch (...) {
@@ -598,7 +630,7 @@ int32_t shk_hip_buffer_create(void* context, uint64_t byte_size, void** out_buff
 int32_t shk_hip_buffer_wrap(void* context, void* device_pointer, uint64_t byte_size, void** out_buffer) {
   if (out_buffer == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "out_buffer is null");
   *out_buffer = nullptr;
-  Context* c = checked<Context, kContextMagic>(context);
+  Context* c = live_context(context);
   if (c == nullptr || (device_pointer == nullptr && byte_size != 0))
     return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid wrap arguments");
   try {
@@ -607,6 +639,7 @@ int32_t shk_hip_buffer_wrap(void* context, void* device_pointer, uint64_t byte_s
     b->ptr = device_pointer;
     b->bytes = byte_size;
     b->owned = false;
+    c->refs.fetch_add(1);
     *out_buffer = b;
     return SHK_HIP_STATUS_OK;
   } catch (...) {
@@ -622,7 +655,9 @@ int32_t shk_hip_buffer_release(void* buffer) {
     (void)hipFree(b->ptr);
   }
   b->magic = 0;
+  Context* c = b->ctx;
   delete b;
+  context_unref(c);
   return SHK_HIP_STATUS_OK;
 }
 
@@ -670,7 +705,7 @@ int32_t shk_hip_buffer_device_pointer(void* buffer, void** out_pointer) {
 int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_bytes, void** out_program) {
   if (out_program == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "out_program is null");
   *out_program = nullptr;
-  Context* c = checked<Context, kContextMagic>(context);
+  Context* c = live_context(context);
   if (c == nullptr || image == nullptr)
     return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid program arguments");
   Program* pr = nullptr;
@@ -689,6 +724,7 @@ int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_
       return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image slot table truncated");
     pr = new Program();
     pr->ctx = c;
+    c->refs.fetch_add(1);
     pr->slots.resize(h.n_slots);
     memcpy(pr->slots.data(), p, h.n_slots * sizeof(SlotRecord));
     p += h.n_slots * sizeof(SlotRecord);

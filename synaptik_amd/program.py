@@ -41,6 +41,7 @@ OP_OPTIMIZER = 11
 OP_STEP_COMMIT = 12
 OP_FILL = 13
 OP_COPY = 14
+OP_TRANSPOSE = 15
 
 ACT = {None: 0, "none": 0, "relu": 1, "tanh": 2, "sigmoid": 3}
 REDUCE_KIND = {"sum": 0, "mean": 1, "max": 2, "lse": 3}
@@ -198,6 +199,10 @@ class ProgramBuilder:
 
     def copy(self, src, dst, n) -> Step:
         return self._add(OP_COPY, [src, dst], [n])
+
+    def transpose(self, X, Y, R, C) -> Step:
+        """Y[C,R] = X[R,C]^T."""
+        return self._add(OP_TRANSPOSE, [X, Y], [R, C])
 
     # ---- encoding ----
     def image(self) -> bytes:

@@ -4,8 +4,8 @@ Workload ("Wide MLP-4096"): 4096 -> 4096 x4 hidden -> 
 MSE loss, SGD momentum 0.9, batch 4096; X, Y ~ N(0,1), He-normal init from a seed; 10 warmup and
 100 timed steps by default. A step is one full training step of the device-resident program:
 5 forward GEMMs with fused bias+ReLU, the MSE loss and gradient, 5 dW GEMMs, 4 dX GEMMs with the
-ReLU gradient fused, 5 bias column sums, and the checked + applied SGD-momentum update of all
-83,906,560 parameters. Inputs are resident in HBM before the timed region; each step is one
+ReLU gradient fused, 5 bias column sums, and the transactional single-pass SGD-momentum update of
+all 83,906,560 parameters into the other half of the double-buffered parameter set. Inputs are resident in HBM before the timed region; each step is one
 synchronous program run (device work complete on return).
 
 Per-step device times come from HIP events recorded on the context stream around every program
@@ -265,9 +265,9 @@ def main() -> int:
         "mse_ms_per_step": round(sum(per.get(OP_MSE, [])), 4),
         "device_ms_per_step": round(sum(step_ms) / runs, 4),
     }
-    # optimizer traffic: check reads p,g,m (12 B), apply reads p,g,m and writes p,m (20 B)
+    # optimizer traffic: one staged pass reads p, g, m and writes the candidate p, m (20 B)
     n_params = spec.parameter_count()
-    opt_gbs = (32.0 * n_params) / (opt_ms * 1e-3) / 1e9 if opt_ms > 0 else None
+    opt_gbs = (20.0 * n_params) / (opt_ms * 1e-3) / 1e9 if opt_ms > 0 else None
     print(f"[bench] breakdown {breakdown}; optimizer {opt_gbs:.0f} GB/s", file=sys.stderr, flush=True)
 
     sess.close()

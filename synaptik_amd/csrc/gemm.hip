@@ -26,9 +26,22 @@
 #include <algorithm>
 #include <cstdlib>
 #include <type_traits>
+#include <utility>
 
 namespace shk {
 namespace {
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [0, N). Keeps accumulator
+// indexing static where a large #pragma unroll body would be left rolled (and the accumulator
+// array demoted to scratch memory).
+template <int... I, typename F>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, I...>, F&& f) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
 
 template <int BM, int BN, int BK, int WM, int WN>
 struct GemmShape {
@@ -146,12 +159,11 @@ gemm_f32_mfma(GemmParams p) {
   TileLoader<BN, BK, NT, PB, TB, VB> lb;
 
   floatx16 acc[MI][NI];
-#pragma unroll
-  for (int i = 0; i < MI; ++i)
-#pragma unroll
-    for (int j = 0; j < NI; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  static_for<MI>([&](auto i) {
+    static_for<NI>([&](auto j) {
+      static_for<16>([&](auto r) { acc[i][j][decltype(r)::value] = 0.f; });
+    });
+  });
 
   const int nk = (int)((p.K + BK - 1) / BK);
   if (nk > 0) {
@@ -189,11 +201,11 @@ gemm_f32_mfma(GemmParams p) {
       // keep the next fragment's reads ahead of this step's MFMAs (the default scheduler sinks
       // them below to save registers, which exposes the LDS latency again)
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < NI; ++j)
+      static_for<MI>([&](auto i) {
+        static_for<NI>([&](auto j) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c][i], b[c][j], acc[i][j], 0, 0, 0);
+        });
+      });
     }
     if (more) {
       la.store(As[cur ^ 1]);
@@ -203,31 +215,35 @@ gemm_f32_mfma(GemmParams p) {
   }
 
   // Epilogue. Accumulator r of a 32x32 block holds row (r/4)*8 + (lane/32)*4 + r%4,
-  // column lane%32 of that block.
-#pragma unroll
-  for (int j = 0; j < NI; ++j) {
+  // column lane%32 of that block. Each block is written from one base pointer with
+  // compile-time row offsets, keeping few address registers live.
+  static_for<NI>([&](auto j) {
     const int64_t col = n0 + wn * (NI * 32) + j * 32 + l32;
-    if (col >= p.N) continue;
-    const float bias = (p.bias != nullptr) ? p.bias[col] : 0.f;
-#pragma unroll
-    for (int i = 0; i < MI; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * (MI * 32) + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-        if (row >= p.M) continue;
-        float v = acc[i][j][r];
-        if (p.mode == 0) {
-          if (p.bias != nullptr) v = v + bias;
-          v = apply_act(p.act, v);
-        } else {
-          v = act_grad(p.act, v, p.aux[row * p.ldaux + col]);
+    const bool col_ok = col < p.N;
+    const float bias = (p.bias != nullptr && col_ok) ? p.bias[col] : 0.f;
+    static_for<MI>([&](auto i) {
+      const int64_t row0 = m0 + wm * (MI * 32) + i * 32 + half * 4;
+      float* cptr = p.C + row0 * p.ldc + col;
+      const float* aptr = p.mode == 1 ? p.aux + row0 * p.ldaux + col : nullptr;
+      static_for<16>([&](auto r) {
+        constexpr int R = decltype(r)::value;
+        constexpr int off = (R >> 2) * 8 + (R & 3);
+        if (col_ok && row0 + off < p.M) {
+          float v = acc[i][j][R];
+          if (p.mode == 0) {
+            if (p.bias != nullptr) v = v + bias;
+            v = apply_act(p.act, v);
+          } else {
+            v = act_grad(p.act, v, aptr[off * p.ldaux]);
+          }
+          float* dst = cptr + off * p.ldc;
+          if (p.accumulate) v = *dst + v;
+          *dst = v;
         }
-        float* dst = p.C + row * p.ldc + col;
-        if (p.accumulate) v = *dst + v;
-        *dst = v;
-      }
-    }
-  }
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  });
 }
 
 // K == 1: every output is exactly one product a*b (CpuMatmulReferenceKernel.java:34-119: a

@@ -97,14 +97,17 @@ struct PwParams {
 hipError_t launch_pointwise(const PwParams& p, hipStream_t s);
 
 // Multi-tensor optimizer. Each entry is one parameter tensor with its gradient and slots.
-constexpr int OPT_MAX_TENSORS = 24;
+constexpr int OPT_MAX_TENSORS = 16;
 struct OptTensor {
   float* p;
   const float* g;
   float* m;
   float* v;
+  float* pn;  // phase 2: candidate parameter / slot buffers (the other half of a double buffer)
+  float* mn;
+  float* vn;
   int64_t n;
-  int64_t start;  // first element index in the concatenated domain
+  int64_t start;  // first block of this tensor in the launch
 };
 struct OptParams {
   OptTensor t[OPT_MAX_TENSORS];
@@ -112,7 +115,8 @@ struct OptParams {
   int64_t total;
   int kind;        // 0 SGD, 1 Adam (coupled decay), 2 AdamW (decoupled decay),
                    // 3 accumulate-sum, 4 commit accumulator, 5 clear accumulator (gated)
-  int phase;       // 0 check (validate every intermediate), 1 apply (commit if status clear)
+  int phase;       // 0 check (validate every intermediate), 1 apply (commit if status clear),
+                   // 2 stage (one pass: write candidates to pn/mn/vn, flag failures)
   float lr, momentum, dampening, weight_decay;  // SGD
   int nesterov, has_momentum_slot;
   float beta1, beta2, eps;                       // Adam

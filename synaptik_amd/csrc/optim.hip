@@ -14,6 +14,12 @@
 // A failed step therefore leaves parameters and optimizer slots bit-for-bit unchanged, and the
 // completed-step counter is advanced only by launch_step_commit when the status stays clear.
 // Traffic: check reads p,g,m(,v); apply reads p,g,m(,v) and writes p,m(,v).
+//
+// With double-buffered parameters and slots one pass suffices:
+//   phase 2 (stage): read the current p,g,m(,v), write every candidate to the other buffer set
+//                    (pn,mn,vn) and flag failures; the host adopts the candidate set only when the
+//                    run returns OK, so a failed step still commits nothing. Traffic 20 B (SGD
+//                    momentum) / 28 B (Adam) per parameter instead of 32 / 44.
 #include "common.h"
 #include "kernels.h"
 
@@ -179,29 +185,59 @@ __global__ void __launch_bounds__(OPT_NT) optimizer_kernel(OptParams p) {
   if (p.kind != 0) k = adam_coeffs(p, completed + 1);
   const int64_t base = ((int64_t)blockIdx.x - T.start) * OPT_CHUNK;
   bool ok = k.ok;
-  if (!k.ok && p.phase == 1) return;
-#pragma unroll
-  for (int q = 0; q < OPT_PER_THREAD; ++q) {
-    const int64_t i = base + q * OPT_NT + threadIdx.x;
-    if (i >= T.n) break;
-    const float pv = T.p[i];
-    const float g = T.g[i];
-    const float mv = T.m != nullptr ? T.m[i] : 0.0f;
-    float pc, mc, vc = 0.0f;
-    bool e;
-    if (p.kind == 0) {
-      e = sgd_element(p, first, pv, g, mv, pc, mc);
-    } else {
-      e = adam_element(p, k, pv, g, mv, T.v[i], pc, mc, vc);
-    }
-    ok &= e;
-    if (p.phase == 1) {
-      T.p[i] = pc;
-      if (T.m != nullptr) T.m[i] = mc;
-      if (p.kind != 0) T.v[i] = vc;
+  // Each thread owns 4 consecutive elements: 128-bit loads and stores when all 4 exist and every
+  // pointer is 16-byte aligned (device allocations and arena slots are), scalar otherwise.
+  const int64_t i0 = base + (int64_t)threadIdx.x * OPT_PER_THREAD;
+  const bool vec = i0 + 3 < T.n &&
+      ((reinterpret_cast<uintptr_t>(T.p) | reinterpret_cast<uintptr_t>(T.g) |
+        reinterpret_cast<uintptr_t>(T.m) | reinterpret_cast<uintptr_t>(T.v) |
+        reinterpret_cast<uintptr_t>(T.pn) | reinterpret_cast<uintptr_t>(T.mn) |
+        reinterpret_cast<uintptr_t>(T.vn)) & 15u) == 0;
+  float pv[4], gv[4], mv[4], vv[4], pc[4], mc[4], vc[4];
+  const int cnt = vec ? 4 : (int)max<int64_t>(0, min<int64_t>(4, T.n - i0));
+  if (vec) {
+    *reinterpret_cast<float4*>(pv) = *reinterpret_cast<const float4*>(T.p + i0);
+    *reinterpret_cast<float4*>(gv) = *reinterpret_cast<const float4*>(T.g + i0);
+    if (T.m != nullptr) *reinterpret_cast<float4*>(mv) = *reinterpret_cast<const float4*>(T.m + i0);
+    if (p.kind != 0) *reinterpret_cast<float4*>(vv) = *reinterpret_cast<const float4*>(T.v + i0);
+  } else {
+    for (int q = 0; q < cnt; ++q) {
+      pv[q] = T.p[i0 + q];
+      gv[q] = T.g[i0 + q];
+      if (T.m != nullptr) mv[q] = T.m[i0 + q];
+      if (p.kind != 0) vv[q] = T.v[i0 + q];
     }
   }
-  if (p.phase == 0) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (q >= cnt) break;
+    const float m0 = T.m != nullptr ? mv[q] : 0.0f;
+    vc[q] = 0.0f;
+    bool e;
+    if (p.kind == 0) {
+      e = sgd_element(p, first, pv[q], gv[q], m0, pc[q], mc[q]);
+    } else {
+      e = adam_element(p, k, pv[q], gv[q], m0, vv[q], pc[q], mc[q], vc[q]);
+    }
+    ok &= e;
+  }
+  if (p.phase != 0) {
+    float* dp = p.phase == 1 ? T.p : T.pn;
+    float* dm = p.phase == 1 ? T.m : T.mn;
+    float* dv = p.phase == 1 ? T.v : T.vn;
+    if (vec) {
+      *reinterpret_cast<float4*>(dp + i0) = *reinterpret_cast<const float4*>(pc);
+      if (dm != nullptr) *reinterpret_cast<float4*>(dm + i0) = *reinterpret_cast<const float4*>(mc);
+      if (p.kind != 0) *reinterpret_cast<float4*>(dv + i0) = *reinterpret_cast<const float4*>(vc);
+    } else {
+      for (int q = 0; q < cnt; ++q) {
+        dp[i0 + q] = pc[q];
+        if (dm != nullptr) dm[i0 + q] = mc[q];
+        if (p.kind != 0) dv[i0 + q] = vc[q];
+      }
+    }
+  }
+  if (p.phase != 1) {
     const int bad = wave_or(ok ? 0 : 1);
     if (bad && (threadIdx.x & 63) == 0)
       atomicOr(p.status, k.ok ? (uint32_t)DEV_NON_FINITE : (uint32_t)DEV_NOT_POSITIVE);

@@ -119,12 +119,13 @@ struct StepRecord {
 };
 struct OptEntry {
   int32_t p, g, m, v;
+  int32_t pn, mn, vn, pad;
   int64_t n;
 };
 #pragma pack(pop)
 static_assert(sizeof(SlotRecord) == 24, "slot record layout");
 static_assert(sizeof(StepRecord) == 200, "step record layout");
-static_assert(sizeof(OptEntry) == 24, "optimizer entry layout");
+static_assert(sizeof(OptEntry) == 40, "optimizer entry layout");
 static_assert(sizeof(shk::PwInstr) == 12, "pointwise instruction layout");
 
 struct Step {
@@ -383,7 +384,7 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
     }
     case OP_OPTIMIZER: {
       const int64_t kind = a[0], phase = a[1];
-      if (kind < 0 || kind > 5 || (phase != 0 && phase != 1))
+      if (kind < 0 || kind > 5 || phase < 0 || phase > 2 || (phase == 2 && kind > 2))
         return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: invalid optimizer", idx);
       if (!v.slot_ok(s[0], false, "step counter") || !v.holds(s[0], 1, DT_I64, "step counter"))
         return v.err;
@@ -397,9 +398,27 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
         if (!v.slot_ok(e[i].p, false, "param") || !v.slot_ok(e[i].g, false, "grad") ||
             !v.slot_ok(e[i].m, !needs_m, "momentum") || !v.slot_ok(e[i].v, !adam, "second moment") ||
             !v.holds(e[i].p, e[i].n, DT_F32, "param") || !v.holds(e[i].g, e[i].n, DT_F32, "grad") ||
-            !v.holds(e[i].m, e[i].n, DT_F32, "momentum") || !v.holds(e[i].v, e[i].n, DT_F32, "second moment") ||
-            !v.writable(e[i].p, "param") || !v.writable(e[i].m, "momentum") || !v.writable(e[i].v, "second moment"))
+            !v.holds(e[i].m, e[i].n, DT_F32, "momentum") || !v.holds(e[i].v, e[i].n, DT_F32, "second moment"))
           return v.err;
+        // writability follows what the step writes: phase 1 updates p,m,v in place; kind 3 writes
+        // p; kinds 4 and 5 write m; phase 0 and phase 2 leave the current tensors untouched
+        const bool in_place = (kind <= 2 && phase == 1);
+        if ((in_place || kind == 3) && !v.writable(e[i].p, "param")) return v.err;
+        if ((in_place || kind >= 4) && !v.writable(e[i].m, "momentum")) return v.err;
+        if (in_place && !v.writable(e[i].v, "second moment")) return v.err;
+        if (phase == 2) {
+          // candidates must exist wherever a current tensor exists
+          if ((e[i].m >= 0) != (e[i].mn >= 0) || (e[i].v >= 0) != (e[i].vn >= 0))
+            return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: staged update lacks a candidate buffer", idx);
+          if (!v.slot_ok(e[i].pn, false, "param candidate") || !v.slot_ok(e[i].mn, true, "momentum candidate") ||
+              !v.slot_ok(e[i].vn, true, "second moment candidate") ||
+              !v.holds(e[i].pn, e[i].n, DT_F32, "param candidate") ||
+              !v.holds(e[i].mn, e[i].n, DT_F32, "momentum candidate") ||
+              !v.holds(e[i].vn, e[i].n, DT_F32, "second moment candidate") ||
+              !v.writable(e[i].pn, "param candidate") || !v.writable(e[i].mn, "momentum candidate") ||
+              !v.writable(e[i].vn, "second moment candidate"))
+            return v.err;
+        }
       }
       return SHK_HIP_STATUS_OK;
     }
@@ -503,6 +522,9 @@ hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipSt
         p.t[i].g = b.get<const float>(e[i].g);
         p.t[i].m = b.get<float>(e[i].m);
         p.t[i].v = b.get<float>(e[i].v);
+        p.t[i].pn = b.get<float>(e[i].pn);
+        p.t[i].mn = b.get<float>(e[i].mn);
+        p.t[i].vn = b.get<float>(e[i].vn);
         p.t[i].n = e[i].n;
       }
       p.kind = (int)a[0]; p.phase = (int)a[1]; p.nesterov = (int)a[2]; p.has_momentum_slot = (int)a[3];

@@ -184,10 +184,22 @@ class ProgramBuilder:
     def optimizer(self, counter, tensors, *, kind: str, phase: int, lr: float, momentum=0.0,
                   dampening=0.0, weight_decay=0.0, nesterov=False, has_momentum_slot=False,
                   beta1=0.9, beta2=0.999, eps=1e-8) -> Step:
-        """tensors: list of (param, grad, m, v, count) slots (m/v None where absent)."""
+        """tensors: list of (param, grad, m, v, count) or, for phase 2 (staged into the other
+        half of a double buffer), (param, grad, m, v, param_next, m_next, v_next, count) slots;
+        absent slots are None. At most 16 tensors per step."""
         k = {"sgd": 0, "adam": 1, "adamw": 2, "acc_sum": 3, "acc_commit": 4, "acc_clear": 5}[kind]
-        payload = b"".join(struct.pack("<iiiiq", _sid(p), _sid(g), _sid(m), _sid(v), int(n))
-                           for (p, g, m, v, n) in tensors)
+        if len(tensors) > 16:
+            raise ValueError("at most 16 tensors per optimizer step")
+        rows = []
+        for t in tensors:
+            if len(t) == 5:
+                p, g, m, v, n = t
+                pn = mn = vn = None
+            else:
+                p, g, m, v, pn, mn, vn, n = t
+            rows.append(struct.pack("<iiiiiiiiq", _sid(p), _sid(g), _sid(m), _sid(v), _sid(pn),
+                                    _sid(mn), _sid(vn), 0, int(n)))
+        payload = b"".join(rows)
         return self._add(OP_OPTIMIZER, [counter], [k, phase, int(nesterov), int(has_momentum_slot)],
                          [lr, momentum, dampening, weight_decay, beta1, beta2, eps], payload)
 

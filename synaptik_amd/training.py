@@ -164,6 +164,11 @@ class TrainingLayout:
     biases: list[Slot] = field(default_factory=list)
     first: list[Slot] = field(default_factory=list)    # momentum / first-moment slots
     second: list[Slot] = field(default_factory=list)   # second-moment slots (Adam)
+    # staged (double-buffered) update: candidate parameter and slot buffers the step writes
+    weights_next: list[Slot] = field(default_factory=list)
+    biases_next: list[Slot] = field(default_factory=list)
+    first_next: list[Slot] = field(default_factory=list)
+    second_next: list[Slot] = field(default_factory=list)
     accum: list[Slot] = field(default_factory=list)    # gradient accumulators (accumulating modes)
     counter: Slot | None = None
     x: Slot | None = None
@@ -184,29 +189,40 @@ def lower_training_step(spec: MlpSpec, batch: int, optimizer, *, label_dtype: st
                         mode: str = GradientMode.RESET_AND_STEP, clear_accumulator: bool = False):
     """Lowers one training step of `spec` at `batch` rows to a program image.
 
-    Inputs (in order): W_1..W_L, b_1..b_L (INOUT), first-moment slots per tensor (INOUT, SGD
-    with momentum and Adam), second-moment slots (INOUT, Adam), gradient accumulators (INOUT,
+    Inputs (in order): W_1..W_L, b_1..b_L (current, read only), first-moment slots per tensor
+    (SGD with momentum and Adam), second-moment slots (Adam); for modes that step, the same
+    tensors again as the candidate set the update writes (INOUT); gradient accumulators (INOUT,
     accumulating modes and RESET_AND_STEP with clear_accumulator), completed-step counter (INOUT,
     int64), x [batch, in], y ([batch, out] f32 for MSE; [batch] int for CE).
     Output: objective [1].
 
-    Every mode is transactional: a non-finite accumulated candidate or optimizer intermediate
-    leaves parameters, slots, accumulators and the counter unchanged.
+    The update is one streaming pass that reads the current set and writes the candidate set; the
+    caller adopts the candidate set only when the run succeeds. Every mode is transactional: a
+    non-finite accumulated candidate or optimizer intermediate leaves the current parameters,
+    slots, accumulators and the counter unchanged.
     """
     kind = _optimizer_kind(optimizer)
     pb = ProgramBuilder()
     lay = TrainingLayout()
     L = len(spec.layers)
+    steps = mode != GradientMode.ACCUMULATE
     for l in spec.layers:
-        lay.weights.append(pb.input(l.fan_in * l.fan_out, inout=True))
+        lay.weights.append(pb.input(l.fan_in * l.fan_out))
     for l in spec.layers:
-        lay.biases.append(pb.input(l.fan_out, inout=True) if l.bias else None)
+        lay.biases.append(pb.input(l.fan_out) if l.bias else None)
     params = lay.weights + [b for b in lay.biases if b is not None]
     has_first = kind != "sgd" or optimizer.momentum != 0.0
     if has_first:
-        lay.first = [pb.input(p.count, inout=True) for p in params]
+        lay.first = [pb.input(p.count) for p in params]
     if kind != "sgd":
-        lay.second = [pb.input(p.count, inout=True) for p in params]
+        lay.second = [pb.input(p.count) for p in params]
+    if steps:
+        lay.weights_next = [pb.input(w.count, inout=True) for w in lay.weights]
+        lay.biases_next = [pb.input(b.count, inout=True) if b is not None else None for b in lay.biases]
+        if has_first:
+            lay.first_next = [pb.input(p.count, inout=True) for p in params]
+        if kind != "sgd":
+            lay.second_next = [pb.input(p.count, inout=True) for p in params]
     uses_acc = mode != GradientMode.RESET_AND_STEP or clear_accumulator
     if uses_acc:
         lay.accum = [pb.input(p.count, inout=True) for p in params]
@@ -258,17 +274,20 @@ def lower_training_step(spec: MlpSpec, batch: int, optimizer, *, label_dtype: st
     if mode != GradientMode.RESET_AND_STEP:
         # G = accumulator + G for every tensor, each candidate checked finite
         acc_entries = [(g, g, a, None, g.count) for g, a in zip(lay.grads, lay.accum)]
-        for i in range(0, len(acc_entries), 24):
-            pb.optimizer(lay.counter, acc_entries[i:i + 24], kind="acc_sum", phase=0, lr=0.0)
+        for i in range(0, len(acc_entries), 16):
+            pb.optimizer(lay.counter, acc_entries[i:i + 16], kind="acc_sum", phase=0, lr=0.0)
         if mode == GradientMode.ACCUMULATE:
-            for i in range(0, len(acc_entries), 24):
-                pb.optimizer(lay.counter, acc_entries[i:i + 24], kind="acc_commit", phase=1, lr=0.0)
+            for i in range(0, len(acc_entries), 16):
+                pb.optimizer(lay.counter, acc_entries[i:i + 16], kind="acc_commit", phase=1, lr=0.0)
             return pb, lay
-    # transactional update: check every tensor, then apply, then advance the counter
+    # one staged pass: current set -> candidate set, failures flagged; then the counter
+    params_next = lay.weights_next + [b for b in lay.biases_next if b is not None]
     entries = []
     for j, p in enumerate(params):
         entries.append((p, lay.grads[j], lay.first[j] if has_first else None,
-                        lay.second[j] if lay.second else None, p.count))
+                        lay.second[j] if lay.second else None, params_next[j],
+                        lay.first_next[j] if has_first else None,
+                        lay.second_next[j] if lay.second else None, p.count))
     common = {}
     if kind == "sgd":
         common = dict(lr=optimizer.learning_rate, momentum=optimizer.momentum,
@@ -277,14 +296,12 @@ def lower_training_step(spec: MlpSpec, batch: int, optimizer, *, label_dtype: st
     else:
         common = dict(lr=optimizer.learning_rate, beta1=optimizer.beta1, beta2=optimizer.beta2,
                       eps=optimizer.epsilon, weight_decay=optimizer.weight_decay)
-    chunks = [entries[i:i + 24] for i in range(0, len(entries), 24)]
-    for phase in (0, 1):
-        for ch in chunks:
-            pb.optimizer(lay.counter, ch, kind=kind, phase=phase, **common)
+    for i in range(0, len(entries), 16):
+        pb.optimizer(lay.counter, entries[i:i + 16], kind=kind, phase=2, **common)
     if uses_acc:
         acc_entries = [(g, g, a, None, g.count) for g, a in zip(lay.grads, lay.accum)]
-        for i in range(0, len(acc_entries), 24):
-            pb.optimizer(lay.counter, acc_entries[i:i + 24], kind="acc_clear", phase=1, lr=0.0)
+        for i in range(0, len(acc_entries), 16):
+            pb.optimizer(lay.counter, acc_entries[i:i + 16], kind="acc_clear", phase=1, lr=0.0)
     pb.step_commit(lay.counter)
     return pb, lay
 
@@ -326,7 +343,10 @@ class TrainingState:
 
 
 class HipTrainingSession:
-    """A prepared, device-resident training step (TrainingSession analogue)."""
+    """A prepared, device-resident training step (TrainingSession analogue).
+
+    Parameters and optimizer slots live in two device buffer sets; a step reads the current set
+    and writes the other, and the session adopts the written set only when the run succeeds."""
 
     def __init__(self, ctx: HipContext, spec: MlpSpec, weights, biases, optimizer, batch: int,
                  *, label_dtype: str = "i64"):
@@ -338,11 +358,17 @@ class HipTrainingSession:
         self._programs: dict[tuple, tuple[HipProgram, TrainingLayout]] = {}
         self.program, lay = self._program(GradientMode.RESET_AND_STEP, False)
         self.layout = lay
-        self.W = [ctx.upload(np.asarray(w, np.float32)) for w in weights]
-        self.b = [ctx.upload(np.asarray(b, np.float32)) for b, l in zip(biases, spec.layers) if l.bias]
-        params = self.W + self.b
-        self.first = [ctx.upload(np.zeros(p.nbytes // 4, np.float32)) for p in params] if lay.first else []
-        self.second = [ctx.upload(np.zeros(p.nbytes // 4, np.float32)) for p in params] if lay.second else []
+        Ws = [np.asarray(w, np.float32) for w in weights]
+        bs = [np.asarray(b, np.float32) for b, l in zip(biases, spec.layers) if l.bias]
+        self._sets = []
+        for _ in range(2):
+            W = [ctx.upload(w) for w in Ws]
+            b = [ctx.upload(x) for x in bs]
+            params = W + b
+            first = [ctx.upload(np.zeros(p.nbytes // 4, np.float32)) for p in params] if lay.first else []
+            second = [ctx.upload(np.zeros(p.nbytes // 4, np.float32)) for p in params] if lay.second else []
+            self._sets.append((W, b, first, second))
+        self._cur = 0
         self.accum: list[HipBuffer] = []
         self.accumulated_gradient_runs = 0
         self.counter = ctx.upload(np.zeros(1, np.int64))
@@ -353,6 +379,23 @@ class HipTrainingSession:
     @classmethod
     def open(cls, ctx, spec, weights, biases, optimizer, batch, **kw) -> "HipTrainingSession":
         return cls(ctx, spec, weights, biases, optimizer, batch, **kw)
+
+    # current set views
+    @property
+    def W(self):
+        return self._sets[self._cur][0]
+
+    @property
+    def b(self):
+        return self._sets[self._cur][1]
+
+    @property
+    def first(self):
+        return self._sets[self._cur][2]
+
+    @property
+    def second(self):
+        return self._sets[self._cur][3]
 
     def _program(self, mode: str, clear: bool):
         key = (mode, clear)
@@ -370,20 +413,26 @@ class HipTrainingSession:
     def run_resident(self, x: HipBuffer, y: HipBuffer,
                      mode: str = GradientMode.RESET_AND_STEP) -> None:
         """One run on device-resident batch buffers; the objective stays on the device."""
+        cur = self._sets[self._cur]
+        nxt = self._sets[1 - self._cur]
+        current = cur[0] + cur[1] + cur[2] + cur[3]
+        candidate = nxt[0] + nxt[1] + nxt[2] + nxt[3]
         pending = self.accumulated_gradient_runs > 0
         if mode == GradientMode.RESET_AND_STEP and not pending:
             prog, _ = self._programs[(mode, False)]
-            prog.run(self.W + self.b + self.first + self.second + [self.counter, x, y], [self.loss])
+            prog.run(current + candidate + [self.counter, x, y], [self.loss])
+            self._cur = 1 - self._cur
             return
         self._ensure_accumulators()
         prog, _ = self._program(mode, mode == GradientMode.RESET_AND_STEP)
-        prog.run(self.W + self.b + self.first + self.second + self.accum + [self.counter, x, y],
-                 [self.loss])
-        # reached only when the program committed
         if mode == GradientMode.ACCUMULATE:
+            prog.run(current + self.accum + [self.counter, x, y], [self.loss])
             self.accumulated_gradient_runs += 1
-        else:
-            self.accumulated_gradient_runs = 0
+            return
+        prog.run(current + candidate + self.accum + [self.counter, x, y], [self.loss])
+        # reached only when the program committed
+        self._cur = 1 - self._cur
+        self.accumulated_gradient_runs = 0
 
     def run(self, x: np.ndarray, y: np.ndarray,
             mode: str = GradientMode.RESET_AND_STEP) -> TrainingStep:

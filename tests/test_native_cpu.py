@@ -77,9 +77,9 @@ def test_image_layout():
     assert list(step[10:22]) == [2, 2, 3, 3, 3, 2, 2, 0, 1, 0, 0, 0]
     off += 200
     step2 = struct.unpack_from("<II8i16q8f", img, off)
-    assert step2[0] == OP_OPTIMIZER and step2[1] == 24
-    assert struct.unpack_from("<iiiiq", img, off + 200) == (1, 0, -1, -1, 6)
-    assert len(img) == off + 200 + 24
+    assert step2[0] == OP_OPTIMIZER and step2[1] == 40
+    assert struct.unpack_from("<iiiiiiiiq", img, off + 200) == (1, 0, -1, -1, -1, -1, -1, 0, 6)
+    assert len(img) == off + 200 + 40
 
 
 def test_training_lowering_structure():
@@ -87,13 +87,13 @@ def test_training_lowering_structure():
     pb, lay = lower_training_step(spec, 4096, Sgd(0.01, momentum=0.9))
     ops = [s.opcode for s in pb.steps]
     assert ops.count(OP_GEMM) == 14  # 5 forward, 5 dW, 4 dX
-    assert ops.count(OP_OPTIMIZER) == 2 and ops[-1] == OP_STEP_COMMIT
+    assert ops.count(OP_OPTIMIZER) == 1 and ops[-1] == OP_STEP_COMMIT
     assert spec.parameter_count() == 83_906_560
-    # inputs: 5 W, 5 b, 10 momentum slots, counter, x, y
-    assert pb.n_inputs == 23 and pb.n_outputs == 1
+    # inputs: current 5 W, 5 b, 10 momentum slots; candidate set of the same 20; counter, x, y
+    assert pb.n_inputs == 43 and pb.n_outputs == 1
     pb2, lay2 = lower_training_step(MlpSpec.chain([784, 1024, 1024, 10], "relu", "ce"), 1024,
                                     Adam(1e-3))
-    assert pb2.n_inputs == 6 + 6 + 6 + 3 and lay2.y.dtype == "i64"
+    assert pb2.n_inputs == 2 * (6 + 6 + 6) + 3 and lay2.y.dtype == "i64"
     fwd = lower_forward(spec, 8)
     assert [s.opcode for s in fwd.steps] == [OP_GEMM] * 5
 

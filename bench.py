@@ -128,7 +128,7 @@ def probe() -> int:
     return 0
 
 
-def secondary(ctx, reps: int = 5) -> dict:
+def secondary(ctx, reps: int = 5, cpu: bool = True) -> dict:
     """The other BASELINE configs, measured on the same context (not the headline value)."""
     from synaptik_amd.native import HipProgram
     from synaptik_amd.program import ProgramBuilder
@@ -203,7 +203,61 @@ def secondary(ctx, reps: int = 5) -> dict:
                                  "ms_per_step": round(wall / 50 * 1e3, 4),
                                  "objective_first": first, "objective_last": float(sess.objective())}
     sess.close()
+    if cpu:
+        add_cpu_baselines(out)
     return out
+
+
+def add_cpu_baselines(out: dict) -> None:
+    """The oracle (1 thread) on bounded samples of the secondary configs, scaled to their units."""
+    from oracle import oracle
+    from synaptik_amd.training import MlpSpec, init_parameters
+    rng = np.random.default_rng(8)
+    # C5: 256 of the 65536 rows, forward (softmax, LSE) and backward
+    rows, C = 256, 4096
+    x = rng.standard_normal((rows, C), dtype=np.float32) * 2
+    g = rng.standard_normal((rows, C), dtype=np.float32)
+    t0 = time.perf_counter()
+    p = oracle.softmax_rows(x)
+    oracle.logsumexp_rows(x)
+    oracle.softmax_grad_rows(p, g)
+    dt = time.perf_counter() - t0
+    gpu_ms = out["c5_softmax_stress"]["fwd_ms"] + out["c5_softmax_stress"]["bwd_ms"]
+    out["c5_softmax_stress"]["cpu_baseline"] = {
+        "rows_per_s": round(rows / dt, 1), "gpu_rows_per_s": round(65536 / (gpu_ms * 1e-3), 1),
+        "cores": 1, "kind": "port", "sample": f"{rows} rows of [65536,4096], fwd+bwd, {dt:.2f} s"}
+    # C2: 256 of the 8192 rows of the fused layer, forward + both backward GEMMs + db
+    B, I, O = 256, 1024, 1024
+    X = rng.standard_normal((B, I), dtype=np.float32)
+    W = rng.standard_normal((I, O), dtype=np.float32) * 0.05
+    dY = rng.standard_normal((B, O), dtype=np.float32)
+    t0 = time.perf_counter()
+    Y = oracle.activation("relu", oracle.matmul(X, W))
+    dZ = oracle.activation_grad("relu", dY, Y)
+    oracle.matmul(dZ, W, trans_b=True)
+    oracle.matmul(X, dZ, trans_a=True)
+    oracle.colsum(dZ)
+    dt = time.perf_counter() - t0
+    out["c2_fused_layer"]["cpu_baseline"] = {
+        "ms_full_layer": round(dt * 8192 / B * 1e3, 1), "cores": 1, "kind": "port",
+        "sample": f"{B} of 8192 rows ({dt:.2f} s), scaled x{8192 // B}"}
+    # C3: one Adam step of the classifier on 64 of the 1024 rows (+ the full update)
+    spec = MlpSpec.chain([784, 1024, 1024, 10], hidden="relu", loss="ce")
+    Ws, bs = init_parameters(spec, 0, "he_normal")
+    model = oracle.OracleMLP(Ws, bs, ["relu", "relu", None], "ce",
+                             dict(kind="adam", lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8))
+    xb = rng.uniform(0, 1, (64, 784)).astype(np.float32)
+    yb = rng.integers(0, 10, 64)
+    t0 = time.perf_counter()
+    model.gradients(xb, yb)
+    t_fb = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    model.step(xb[:1], yb[:1])
+    t_one = time.perf_counter() - t0  # dominated by the full-parameter Adam stage
+    step_s = t_fb * 1024 / 64 + t_one
+    out["c3_classifier_adam"]["cpu_baseline"] = {
+        "samples_per_s": round(1024 / step_s, 1), "cores": 1, "kind": "port",
+        "sample": f"fwd+bwd on 64 of 1024 rows scaled x16 ({t_fb:.2f} s) + one full Adam step ({t_one:.2f} s)"}
 
 
 def main() -> int:
@@ -271,7 +325,7 @@ def main() -> int:
     print(f"[bench] breakdown {breakdown}; optimizer {opt_gbs:.0f} GB/s", file=sys.stderr, flush=True)
 
     sess.close()
-    extra = None if args.no_secondary else secondary(ctx)
+    extra = None if args.no_secondary else secondary(ctx, cpu=args.cpu_sample > 0)
     if extra:
         print(f"[bench] secondary {extra}", file=sys.stderr, flush=True)
     cpu = None

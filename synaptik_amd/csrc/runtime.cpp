@@ -246,9 +246,10 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
         return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid GEMM attributes", idx);
       if (M > INT32_MAX / 2 || N > INT32_MAX / 2)
         return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: GEMM extent too large", idx);
-      if ((K > 0 && (tA ? lda < std::max<int64_t>(M, 1) : lda < K)) ||
+      const bool empty = M == 0 || N == 0;  // touches no memory
+      if (!empty && ((K > 0 && (tA ? lda < std::max<int64_t>(M, 1) : lda < K)) ||
           (K > 0 && (tB ? ldb < K : ldb < std::max<int64_t>(N, 1))) ||
-          ldc < std::max<int64_t>(N, 1) || (mode == 1 && ldaux < std::max<int64_t>(N, 1)))
+          ldc < std::max<int64_t>(N, 1) || (mode == 1 && ldaux < std::max<int64_t>(N, 1))))
         return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: GEMM leading dimension too small", idx);
       if (mode == 1 && s[4] < 0)
         return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: activation gradient needs aux", idx);

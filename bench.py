@@ -265,7 +265,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--cpu-sample", type=int, default=16, help="rows for the CPU baseline (0 = skip)")
+    ap.add_argument("--cpu-sample", type=int, default=64, help="rows for the CPU baseline (0 = skip)")
     ap.add_argument("--no-secondary", action="store_true", help="skip the C2/C3/C5 lines")
     ap.add_argument("--probe", action="store_true",
                     help="counter probe: 3 launches each of one 4096^3 NT GEMM and a 256 MiB copy")

@@ -38,72 +38,114 @@ enum PwOp : uint8_t {
 };
 constexpr int PW_REGS = 8;
 
-__device__ __forceinline__ float pw_load(const PwParams& p, int k, int64_t row, int64_t col) {
-  switch (p.in_mode[k]) {
-    case 1: return p.in[k][col];
-    case 2: return p.in[k][row];
-    case 3: return p.in[k][0];
-    default: return p.in[k][row * p.C + col];
-  }
-}
+// Binary64-evaluated transcendentals kept out of line: they are rare in chains, and inlining
+// them into every interpreter case inflates the register allocation of the whole kernel.
+__device__ __noinline__ float pw_tanh(float a) { return tanh_f(a); }
+__device__ __noinline__ float pw_sigmoid(float a) { return sigmoid_f(a); }
+__device__ __noinline__ float pw_exp(float a) { return (float)exp((double)a); }
+__device__ __noinline__ float pw_log(float a) { return (float)log((double)a); }
+__device__ __noinline__ float pw_sqrt(float a) { return (float)sqrt((double)a); }
 
-__device__ __forceinline__ void pw_exec(const PwParams& p, float (&r)[PW_REGS][4], int64_t e0,
-                                        int cnt, float (&outv)[PW_MAX_OUTPUTS][4]) {
-  for (int pc = 0; pc < p.n_instr; ++pc) {
-    const PwInstr ins = p.code[pc];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (q >= cnt) break;
-      float& d = r[ins.dst & (PW_REGS - 1)][q];
-      const float a = r[ins.a & (PW_REGS - 1)][q];
-      const float b = r[ins.b & (PW_REGS - 1)][q];
-      switch (ins.op) {
-        case PW_LOAD: {
-          const int64_t e = e0 + q;
-          const int k = ins.a % PW_MAX_INPUTS;
-          if (p.in_mode[k] == 0) {
-            d = p.in[k][e];
-          } else if (p.in_mode[k] == 3) {
-            d = p.in[k][0];
-          } else {
-            const int64_t row = e / p.C;
-            d = pw_load(p, k, row, e - row * p.C);
-          }
-          break;
-        }
-        case PW_CONST: d = ins.imm; break;
-        case PW_ADD: d = a + b; break;
-        case PW_SUB: d = a - b; break;
-        case PW_MUL: d = a * b; break;
-        case PW_DIV: d = a / b; break;
-        case PW_NEG: d = -a; break;
-        case PW_RELU: d = relu_f(a); break;
-        case PW_TANH: d = tanh_f(a); break;
-        case PW_SIGMOID: d = sigmoid_f(a); break;
-        case PW_EXP: d = (float)exp((double)a); break;
-        case PW_LOG: d = (float)log((double)a); break;
-        case PW_RELU_GRAD: d = act_grad(ACT_RELU, b, a); break;
-        case PW_TANH_GRAD: d = act_grad(ACT_TANH, b, a); break;
-        case PW_SIGMOID_GRAD: d = act_grad(ACT_SIGMOID, b, a); break;
-        case PW_GT: d = a > b ? 1.0f : 0.0f; break;
-        case PW_WHERE: d = (r[ins.c & (PW_REGS - 1)][q] != 0.0f) ? a : b; break;
-        case PW_STORE: outv[ins.dst & 1][q] = a; break;
-        case PW_MAX: d = java_max(a, b); break;
-        case PW_SQRT: d = (float)sqrt((double)a); break;
-        default: break;
+// Loads input k for the 4-element group starting at e0 (cnt valid elements) into v.
+__device__ __forceinline__ void pw_load4(const PwParams& p, int k, int64_t e0, int cnt, float (&v)[4]) {
+  const float* src = p.in[k];
+  switch (p.in_mode[k]) {
+    case 0:
+      if (cnt == 4 && (reinterpret_cast<uintptr_t>(src + e0) & 15u) == 0) {
+        const float4 t = *reinterpret_cast<const float4*>(src + e0);
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+      } else {
+        for (int q = 0; q < cnt; ++q) v[q] = src[e0 + q];
+      }
+      break;
+    case 3: {
+      const float t = src[0];
+      v[0] = v[1] = v[2] = v[3] = t;
+      break;
+    }
+    default: {
+      // one division per group, then walk (row, col) forward
+      int64_t row = e0 / p.C, col = e0 - row * p.C;
+      for (int q = 0; q < cnt; ++q) {
+        v[q] = p.in_mode[k] == 1 ? src[col] : src[row];
+        if (++col == p.C) { col = 0; ++row; }
       }
     }
   }
 }
 
-__global__ void __launch_bounds__(256) pointwise_kernel(PwParams p) {
+// The interpreter's register file lives in LDS: register k of thread t holds its 4 elements at
+// regs[k][t*4 .. t*4+3]. Any register index is then just an address (no dynamically indexed
+// VGPR array, no scratch), and each operand access is one 128-bit LDS access per lane.
+constexpr int PW_NT = 256;
+struct PwRegs {
+  float4 v[PW_REGS][PW_NT];
+};
+
+__device__ __forceinline__ void pw_exec(const PwParams& p, PwRegs& R, int64_t e0, int cnt,
+                                        float (&outv)[PW_MAX_OUTPUTS][4]) {
+  const int t = threadIdx.x;
+  for (int pc = 0; pc < p.n_instr; ++pc) {
+    const PwInstr ins = p.code[pc];
+    float4& d4 = R.v[ins.dst & (PW_REGS - 1)][t];
+    if (ins.op == PW_LOAD) {
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      pw_load4(p, ins.a % PW_MAX_INPUTS, e0, cnt, v);
+      d4 = make_float4(v[0], v[1], v[2], v[3]);
+      continue;
+    }
+    const float4 a4 = R.v[ins.a & (PW_REGS - 1)][t];
+    const float4 b4 = R.v[ins.b & (PW_REGS - 1)][t];
+    const float a[4] = {a4.x, a4.y, a4.z, a4.w};
+    const float b[4] = {b4.x, b4.y, b4.z, b4.w};
+    float c[4] = {0.f, 0.f, 0.f, 0.f};
+    if (ins.op == PW_WHERE) {
+      const float4 c4 = R.v[ins.c & (PW_REGS - 1)][t];
+      c[0] = c4.x; c[1] = c4.y; c[2] = c4.z; c[3] = c4.w;
+    }
+    float d[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      switch (ins.op) {
+        case PW_CONST: d[q] = ins.imm; break;
+        case PW_ADD: d[q] = a[q] + b[q]; break;
+        case PW_SUB: d[q] = a[q] - b[q]; break;
+        case PW_MUL: d[q] = a[q] * b[q]; break;
+        case PW_DIV: d[q] = a[q] / b[q]; break;
+        case PW_NEG: d[q] = -a[q]; break;
+        case PW_RELU: d[q] = relu_f(a[q]); break;
+        case PW_TANH: d[q] = pw_tanh(a[q]); break;
+        case PW_SIGMOID: d[q] = pw_sigmoid(a[q]); break;
+        case PW_EXP: d[q] = pw_exp(a[q]); break;
+        case PW_LOG: d[q] = pw_log(a[q]); break;
+        case PW_RELU_GRAD: d[q] = act_grad(ACT_RELU, b[q], a[q]); break;
+        case PW_TANH_GRAD: d[q] = act_grad(ACT_TANH, b[q], a[q]); break;
+        case PW_SIGMOID_GRAD: d[q] = act_grad(ACT_SIGMOID, b[q], a[q]); break;
+        case PW_GT: d[q] = a[q] > b[q] ? 1.0f : 0.0f; break;
+        case PW_WHERE: d[q] = (c[q] != 0.0f) ? a[q] : b[q]; break;
+        case PW_STORE: d[q] = a[q]; break;
+        case PW_MAX: d[q] = java_max(a[q], b[q]); break;
+        case PW_SQRT: d[q] = pw_sqrt(a[q]); break;
+        default: d[q] = 0.0f; break;
+      }
+    }
+    if (ins.op == PW_STORE) {
+      float* o = outv[ins.dst & 1];
+      o[0] = d[0]; o[1] = d[1]; o[2] = d[2]; o[3] = d[3];
+    } else {
+      d4 = make_float4(d[0], d[1], d[2], d[3]);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(PW_NT) pointwise_kernel(PwParams p) {
+  __shared__ PwRegs regs;
   const int64_t n = p.R * p.C;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x * 4;
   for (int64_t e0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; e0 < n; e0 += stride) {
     const int cnt = (int)min<int64_t>(4, n - e0);
-    float r[PW_REGS][4];
-    float outv[PW_MAX_OUTPUTS][4];
-    pw_exec(p, r, e0, cnt, outv);
+    float outv[PW_MAX_OUTPUTS][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    pw_exec(p, regs, e0, cnt, outv);
     // Stores: vectorized when the group is complete and aligned.
 #pragma unroll
     for (int o = 0; o < PW_MAX_OUTPUTS; ++o) {
@@ -267,7 +309,7 @@ unsigned grid_for(int64_t n, int per_thread, int nt = 256) {
 hipError_t launch_pointwise(const PwParams& p, hipStream_t s) {
   const int64_t n = p.R * p.C;
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(pointwise_kernel, dim3(grid_for(n, 4)), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(pointwise_kernel, dim3(grid_for(n, 4)), dim3(PW_NT), 0, s, p);
   return hipGetLastError();
 }
 

@@ -165,10 +165,13 @@ gemm_f32_mfma(GemmParams p) {
     });
   });
 
-  const int nk = (int)((p.K + BK - 1) / BK);
+  // K slice of this block row (the whole of K unless split-K is active)
+  const int64_t k_begin = p.kchunk > 0 ? (int64_t)blockIdx.y * p.kchunk : 0;
+  const int64_t k_end = p.kchunk > 0 ? min(p.K, k_begin + p.kchunk) : p.K;
+  const int nk = k_end > k_begin ? (int)((k_end - k_begin + BK - 1) / BK) : 0;
   if (nk > 0) {
-    la.load(p.A, p.lda, m0, 0, p.M, p.K);
-    lb.load(p.B, p.ldb, n0, 0, p.N, p.K);
+    la.load(p.A, p.lda, m0, k_begin, p.M, k_end);
+    lb.load(p.B, p.ldb, n0, k_begin, p.N, k_end);
     la.store(As[0]);
     lb.store(Bs[0]);
     __syncthreads();
@@ -177,8 +180,8 @@ gemm_f32_mfma(GemmParams p) {
     const int cur = kt & 1;
     const bool more = kt + 1 < nk;
     if (more) {
-      la.load(p.A, p.lda, m0, (int64_t)(kt + 1) * BK, p.M, p.K);
-      lb.load(p.B, p.ldb, n0, (int64_t)(kt + 1) * BK, p.N, p.K);
+      la.load(p.A, p.lda, m0, k_begin + (int64_t)(kt + 1) * BK, p.M, k_end);
+      lb.load(p.B, p.ldb, n0, k_begin + (int64_t)(kt + 1) * BK, p.N, k_end);
     }
     const float* a_s = As[cur] + wm * (MI * 32) + l32 + half * PA;
     const float* b_s = Bs[cur] + wn * (NI * 32) + l32 + half * PB;
@@ -217,6 +220,22 @@ gemm_f32_mfma(GemmParams p) {
   // Epilogue. Accumulator r of a 32x32 block holds row (r/4)*8 + (lane/32)*4 + r%4,
   // column lane%32 of that block. Each block is written from one base pointer with
   // compile-time row offsets, keeping few address registers live.
+  if (p.partial != nullptr) {
+    // split-K: raw partial sums, reduced (and given the epilogue) by gemm_splitk_reduce
+    float* part = p.partial + (int64_t)blockIdx.y * p.M * p.N;
+    static_for<NI>([&](auto j) {
+      const int64_t col = n0 + wn * (NI * 32) + j * 32 + l32;
+      static_for<MI>([&](auto i) {
+        const int64_t row0 = m0 + wm * (MI * 32) + i * 32 + half * 4;
+        static_for<16>([&](auto r) {
+          constexpr int R = decltype(r)::value;
+          constexpr int off = (R >> 2) * 8 + (R & 3);
+          if (col < p.N && row0 + off < p.M) part[(row0 + off) * p.N + col] = acc[i][j][R];
+        });
+      });
+    });
+    return;
+  }
   static_for<NI>([&](auto j) {
     const int64_t col = n0 + wn * (NI * 32) + j * 32 + l32;
     const bool col_ok = col < p.N;
@@ -268,12 +287,34 @@ __global__ void __launch_bounds__(256) gemm_k1_outer(GemmParams p) {
   }
 }
 
+// Split-K reduction: sums the slices of each output in slice order (a fixed binary32 order, so
+// results are deterministic) and applies the GEMM epilogue.
+__global__ void __launch_bounds__(256) gemm_splitk_reduce(GemmParams p, int splits) {
+  const int64_t total = p.M * p.N;
+  const int64_t plane = total;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int64_t row = e / p.N, col = e - row * p.N;
+    float v = p.partial[e];
+    for (int sidx = 1; sidx < splits; ++sidx) v = v + p.partial[sidx * plane + e];
+    if (p.mode == 0) {
+      if (p.bias != nullptr) v = v + p.bias[col];
+      v = apply_act(p.act, v);
+    } else {
+      v = act_grad(p.act, v, p.aux[row * p.ldaux + col]);
+    }
+    float* dst = p.C + row * p.ldc + col;
+    if (p.accumulate) v = *dst + v;
+    *dst = v;
+  }
+}
+
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB,
           int MINW = (BM / WM) * (BN / WN) >= 8 ? 2 : 1>
 hipError_t launch_cfg(const GemmParams& p, bool va, bool vb, hipStream_t s) {
   using S = GemmShape<BM, BN, BK, WM, WN>;
   const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  dim3 grid((unsigned)tiles), block(S::NT);
+  const int64_t splits = p.kchunk > 0 ? (p.K + p.kchunk - 1) / p.kchunk : 1;
+  dim3 grid((unsigned)tiles, (unsigned)splits), block(S::NT);
   if (va && vb)
     hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, TA, TB, true, true, MINW>), grid, block, 0, s, p);
   else if (va)
@@ -333,8 +374,55 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 
 }  // namespace
 
-hipError_t launch_gemm(const GemmParams& p, hipStream_t s) {
+namespace {
+// Split-K plan for problems too small to give every CU a 128x128 tile: slices of at least 128 of
+// K, enough of them to reach ~256 workgroups, at most 16.
+int64_t splitk_slices(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  if (K < 512 || tiles >= 128) return 1;
+  int64_t s = (256 + tiles - 1) / tiles;
+  s = std::min<int64_t>(s, 16);
+  s = std::min<int64_t>(s, K / 128);
+  return std::max<int64_t>(s, 1);
+}
+int64_t splitk_chunk(int64_t K, int64_t s) {
+  const int64_t c = (K + s - 1) / s;
+  return ((c + 15) / 16) * 16;  // whole BK tiles per slice
+}
+}  // namespace
+
+int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 1) return 0;
+  const int64_t s = splitk_slices(M, N, K);
+  if (s <= 1) return 0;
+  const int64_t slices = (K + splitk_chunk(K, s) - 1) / splitk_chunk(K, s);
+  return slices * M * N;
+}
+
+hipError_t launch_gemm(const GemmParams& in, float* workspace, hipStream_t s) {
+  GemmParams p = in;
+  p.partial = nullptr;
+  p.kchunk = 0;
   if (p.M <= 0 || p.N <= 0) return hipSuccess;
+  if (workspace != nullptr && p.K > 1 && splitk_slices(p.M, p.N, p.K) > 1) {
+    p.kchunk = splitk_chunk(p.K, splitk_slices(p.M, p.N, p.K));
+    const int slices = (int)((p.K + p.kchunk - 1) / p.kchunk);
+    p.partial = workspace;
+    const int64_t a_contig = p.transA ? p.M : p.K;
+    const int64_t b_contig = p.transB ? p.K : p.N;
+    const bool va = a_contig % 4 == 0 && p.lda % 4 == 0 && aligned16(p.A);
+    const bool vb = b_contig % 4 == 0 && p.ldb % 4 == 0 && aligned16(p.B);
+    hipError_t e;
+    if (!p.transA && !p.transB) e = launch_cfg<128, 128, 16, 64, 64, false, false>(p, va, vb, s);
+    else if (!p.transA && p.transB) e = launch_cfg<128, 128, 16, 64, 64, false, true>(p, va, vb, s);
+    else if (p.transA && !p.transB) e = launch_cfg<128, 128, 16, 64, 64, true, false>(p, va, vb, s);
+    else e = launch_cfg<128, 128, 16, 64, 64, true, true>(p, va, vb, s);
+    if (e != hipSuccess) return e;
+    const int64_t total = p.M * p.N;
+    const unsigned blocks = (unsigned)std::min<int64_t>(65536, (total + 255) / 256);
+    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(blocks), dim3(256), 0, s, p, slices);
+    return hipGetLastError();
+  }
   if (p.K == 1) {
     const int64_t total = p.M * p.N;
     const unsigned blocks = (unsigned)std::min<int64_t>(65536, (total + 255) / 256);

@@ -31,8 +31,15 @@ struct GemmParams {
   int64_t lda, ldb, ldc, ldaux;
   int transA, transB;
   int act, mode, accumulate;
+  // Split-K (set by launch_gemm, not by callers): block row y handles K slice
+  // [y*kchunk, min(K, (y+1)*kchunk)) and writes raw partial sums to partial[y][M][N].
+  float* partial;
+  int64_t kchunk;
 };
-hipError_t launch_gemm(const GemmParams& p, hipStream_t s);
+// `workspace` holds at least gemm_workspace_floats(M, N, K) floats (split-K partials); it may be
+// null when that is 0.
+hipError_t launch_gemm(const GemmParams& p, float* workspace, hipStream_t s);
+int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K);
 
 // Column sums of X[R,N] (row stride ldx) into out[N]; out = (float)(sum * scale_num / scale_den)
 // with the sum accumulated in binary64. Used for SUM_TO_SHAPE (bias gradients) and MEAN.

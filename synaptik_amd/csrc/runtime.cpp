@@ -261,6 +261,7 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
           !v.holds(s[2], span(M, N, ldc), DT_F32, "C") || !v.holds(s[3], N, DT_F32, "bias") ||
           !v.holds(s[4], span(M, N, ldaux), DT_F32, "aux") || !v.writable(s[2], "C"))
         return v.err;
+      need((uint64_t)((shk::gemm_workspace_floats(M, N, K) + 1) / 2));  // floats in double units
       return SHK_HIP_STATUS_OK;
     }
     case OP_COLSUM: {
@@ -476,7 +477,7 @@ hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipSt
       p.lda = a[3]; p.ldb = a[4]; p.ldc = a[5]; p.ldaux = a[6];
       p.transA = (int)a[7]; p.transB = (int)a[8];
       p.act = (int)a[9]; p.mode = (int)a[10]; p.accumulate = (int)a[11];
-      return shk::launch_gemm(p, stream);
+      return shk::launch_gemm(p, reinterpret_cast<float*>(pr.scratch), stream);
     }
     case OP_COLSUM:
       return shk::launch_colsum(b.get<const float>(s[0]), b.get<float>(s[1]), a[0], a[1], a[2],

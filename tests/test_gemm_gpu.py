@@ -104,3 +104,27 @@ def test_gemm_empty_contraction_is_positive_zero(ctx):
     pb.gemm(sa, sb, sc, M, N, 0)
     (C,) = run_program(ctx, pb, [np.zeros(1, np.float32), np.zeros(1, np.float32)], [sc])
     assert np.array_equal(C.view(np.uint32), np.zeros(M * N, np.uint32))
+
+
+@pytest.mark.parametrize("act", ["relu", "tanh", None])
+@pytest.mark.parametrize("K", [1000, 4096])
+def test_split_k_epilogues(ctx, act, K):
+    """Shapes with too few tiles for the chip take the split-K path (slices reduced in a fixed
+    order): integer operands keep it bit-exact, with the bias/activation applied after the sum."""
+    M, N = 200, 96
+    rng = np.random.default_rng(K)
+    X = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    W = rng.integers(-3, 4, size=(N, K)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    Y = _gemm_case(ctx, X, W, M, N, K, False, True, bias=b, act=act)
+    assert np.array_equal(Y, oracle.linear_forward(X, W, b, act))
+
+
+def test_split_k_activation_gradient(ctx):
+    M, N, K = 130, 72, 2048
+    rng = np.random.default_rng(13)
+    dZ = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    W = rng.integers(-3, 4, size=(K, N)).astype(np.float32)
+    y = oracle.activation("sigmoid", rng.standard_normal((M, N)).astype(np.float32))
+    out = _gemm_case(ctx, dZ, W, M, N, K, False, False, aux=y, act="sigmoid", act_grad=True)
+    assert np.array_equal(out, oracle.activation_grad("sigmoid", oracle.matmul(dZ, W), y))

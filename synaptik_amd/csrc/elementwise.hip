@@ -176,19 +176,27 @@ __global__ void copy_kernel(const float* __restrict__ s, float* __restrict__ d, 
     d[i] = s[i];
 }
 
-// Column sums, pass 1: block (cx, ry) sums a 64-column x CHUNK-row panel; each of the 4 waves
-// walks a quarter of the rows with lanes on consecutive columns (coalesced 256 B rows).
+// Column sums, pass 1: block (cx, ry) sums a 64-column x `rows`-row panel; each of the 4 waves
+// walks a quarter of the panel's rows with lanes on consecutive columns (coalesced 256 B rows).
+// The panel height is chosen per call so that a launch has ~1024 blocks even for short inputs.
 constexpr int CS_COLS = 64;
-constexpr int CS_ROWS = 256;  // rows per panel
+constexpr int64_t CS_TARGET_BLOCKS = 1024;
+int64_t colsum_rows_per_panel(int64_t R, int64_t N) {
+  const int64_t colblocks = (N + CS_COLS - 1) / CS_COLS;
+  const int64_t panels = std::max<int64_t>(1, (CS_TARGET_BLOCKS + colblocks - 1) / colblocks);
+  int64_t rows = (R + panels - 1) / panels;
+  rows = std::max<int64_t>(64, ((rows + 3) / 4) * 4);
+  return rows;
+}
 __global__ void __launch_bounds__(256) colsum_pass1(const float* __restrict__ x, double* part,
-                                                   int64_t R, int64_t N, int64_t ldx) {
+                                                   int64_t R, int64_t N, int64_t ldx, int64_t rows) {
   __shared__ double lds[4][CS_COLS];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t col = (int64_t)blockIdx.x * CS_COLS + lane;
-  const int64_t r0 = (int64_t)blockIdx.y * CS_ROWS;
+  const int64_t r0 = (int64_t)blockIdx.y * rows;
   double s = 0.0;
   if (col < N) {
-    const int64_t rend = min<int64_t>(R, r0 + CS_ROWS);
+    const int64_t rend = min<int64_t>(R, r0 + rows);
     for (int64_t r = r0 + w; r < rend; r += 4) s += (double)x[r * ldx + col];
   }
   lds[w][lane] = s;
@@ -337,15 +345,17 @@ hipError_t launch_copy(const float* src, float* dst, int64_t n, hipStream_t s) {
 }
 
 int64_t colsum_partial_doubles(int64_t R, int64_t N) {
-  return ((R + CS_ROWS - 1) / CS_ROWS) * N;
+  const int64_t rows = colsum_rows_per_panel(R, N);
+  return ((R + rows - 1) / rows) * N;
 }
 hipError_t launch_colsum(const float* x, float* out, int64_t R, int64_t N, int64_t ldx,
                          double divisor, int accumulate, double* partial, hipStream_t s) {
   if (N <= 0) return hipSuccess;
-  const int64_t P = (R + CS_ROWS - 1) / CS_ROWS;
+  const int64_t rows = colsum_rows_per_panel(R, N);
+  const int64_t P = (R + rows - 1) / rows;
   if (P > 0) {
     dim3 g1((unsigned)((N + CS_COLS - 1) / CS_COLS), (unsigned)P);
-    hipLaunchKernelGGL(colsum_pass1, g1, dim3(256), 0, s, x, partial, R, N, ldx);
+    hipLaunchKernelGGL(colsum_pass1, g1, dim3(256), 0, s, x, partial, R, N, ldx, rows);
   }
   hipLaunchKernelGGL(colsum_pass2, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s, partial,
                      out, P, N, divisor, accumulate);

@@ -13,6 +13,8 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
+#include <map>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -145,6 +147,10 @@ struct Program {
   double* scratch = nullptr;              // reduction partials
   uint32_t* status = nullptr;             // device status word (inside the arena)
   std::mutex run_mutex;
+  // HIP-graph replay: the whole step sequence captured once per distinct set of bound pointers
+  bool graphs = true;
+  std::map<std::vector<void*>, hipGraphExec_t> graph_cache;
+  std::vector<std::vector<void*>> graph_order;  // insertion order, for eviction
   bool profiling = false;
   uint64_t profiled_runs = 0;
   std::vector<double> step_ms;
@@ -551,6 +557,7 @@ hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipSt
 
 void destroy_program(Program* p) {
   if (p == nullptr) return;
+  for (auto& kv : p->graph_cache) (void)hipGraphExecDestroy(kv.second);
   for (hipEvent_t e : p->events) (void)hipEventDestroy(e);
   if (p->arena != nullptr) (void)hipFree(p->arena);
   p->magic = 0;
@@ -833,6 +840,10 @@ int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_
     pr->status = static_cast<uint32_t*>(pr->arena);
     pr->scratch = reinterpret_cast<double*>(static_cast<char*>(pr->arena) + scratch_off);
     pr->step_ms.assign(h.n_steps, 0.0);
+    {
+      const char* g = getenv("SHK_HIP_GRAPHS");
+      pr->graphs = !(g != nullptr && g[0] == '0');
+    }
     *out_program = pr;
     return SHK_HIP_STATUS_OK;
   } catch (const std::bad_alloc&) {
@@ -860,6 +871,14 @@ int32_t shk_hip_program_arena_bytes(void* program, uint64_t* out_bytes) {
   Program* pr = checked<Program, kProgramMagic>(program);
   if (pr == nullptr || out_bytes == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid arguments");
   *out_bytes = pr->arena_bytes;
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_program_set_graph_mode(void* program, int32_t enabled) {
+  Program* pr = checked<Program, kProgramMagic>(program);
+  if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
+  std::lock_guard<std::mutex> lock(pr->run_mutex);
+  pr->graphs = enabled != 0;
   return SHK_HIP_STATUS_OK;
 }
 
@@ -948,17 +967,58 @@ int32_t shk_hip_program_run(void* program, uint32_t input_count, void* const* in
     std::lock_guard<std::mutex> ctx_lock(pr->ctx->mutex);
     HIP_TRY(hipSetDevice(pr->ctx->device));
     hipStream_t stream = pr->ctx->stream;
-    HIP_TRY(shk::launch_fill_u32(pr->status, 4, 0u, stream));
-    for (size_t i = 0; i < pr->steps.size(); ++i) {
-      if (pr->profiling) HIP_TRY(hipEventRecord(pr->events[i], stream));
-      const hipError_t e = enqueue_step(*pr, pr->steps[i], b, stream);
-      if (e != hipSuccess) {
-        (void)hipStreamSynchronize(stream);
-        return fail(SHK_HIP_STATUS_EXECUTION_FAILED, "step %zu (opcode %u) launch failed: %s", i,
-                    pr->steps[i].rec.opcode, hipGetErrorName(e));
+    bool launched = false;
+    if (pr->graphs && !pr->profiling) {
+      auto it = pr->graph_cache.find(b.ptr);
+      if (it == pr->graph_cache.end()) {
+        // capture: status clear (a fill kernel, no memset node) + every step
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        bool ok = hipStreamBeginCapture(stream, hipStreamCaptureModeRelaxed) == hipSuccess;
+        if (ok) {
+          bool steps_ok = shk::launch_fill_u32(pr->status, 4, 0u, stream) == hipSuccess;
+          for (size_t i = 0; steps_ok && i < pr->steps.size(); ++i)
+            steps_ok = enqueue_step(*pr, pr->steps[i], b, stream) == hipSuccess;
+          const bool ended = hipStreamEndCapture(stream, &graph) == hipSuccess;
+          ok = steps_ok && ended && graph != nullptr &&
+               hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess;
+          if (graph != nullptr) (void)hipGraphDestroy(graph);
+        }
+        (void)hipGetLastError();  // a failed capture falls back to direct launches
+        if (ok) {
+          if (pr->graph_order.size() >= 8) {
+            auto old = pr->graph_cache.find(pr->graph_order.front());
+            if (old != pr->graph_cache.end()) {
+              (void)hipGraphExecDestroy(old->second);
+              pr->graph_cache.erase(old);
+            }
+            pr->graph_order.erase(pr->graph_order.begin());
+          }
+          it = pr->graph_cache.emplace(b.ptr, exec).first;
+          pr->graph_order.push_back(b.ptr);
+        } else {
+          if (exec != nullptr) (void)hipGraphExecDestroy(exec);
+          pr->graphs = false;
+        }
+      }
+      if (it != pr->graph_cache.end()) {
+        HIP_TRY(hipGraphLaunch(it->second, stream));
+        launched = true;
       }
     }
-    if (pr->profiling) HIP_TRY(hipEventRecord(pr->events[pr->steps.size()], stream));
+    if (!launched) {
+      HIP_TRY(shk::launch_fill_u32(pr->status, 4, 0u, stream));
+      for (size_t i = 0; i < pr->steps.size(); ++i) {
+        if (pr->profiling) HIP_TRY(hipEventRecord(pr->events[i], stream));
+        const hipError_t e = enqueue_step(*pr, pr->steps[i], b, stream);
+        if (e != hipSuccess) {
+          (void)hipStreamSynchronize(stream);
+          return fail(SHK_HIP_STATUS_EXECUTION_FAILED, "step %zu (opcode %u) launch failed: %s", i,
+                      pr->steps[i].rec.opcode, hipGetErrorName(e));
+        }
+      }
+      if (pr->profiling) HIP_TRY(hipEventRecord(pr->events[pr->steps.size()], stream));
+    }
     HIP_TRY(hipMemcpyAsync(pr->ctx->host_status, pr->status, 4, hipMemcpyDeviceToHost, stream));
     const hipError_t se = hipStreamSynchronize(stream);
     if (se != hipSuccess)

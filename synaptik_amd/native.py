@@ -60,6 +60,7 @@ EXPORTED_SYMBOLS = (
     "shk_hip_program_set_profiling",
     "shk_hip_program_step_times",
     "shk_hip_program_step_count",
+    "shk_hip_program_set_graph_mode",
 )
 
 
@@ -128,6 +129,7 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
             "shk_hip_program_step_times": (i32, [vp, ctypes.POINTER(ctypes.c_double), u32,
                                                  ctypes.POINTER(u64)]),
             "shk_hip_program_step_count": (i32, [vp, ctypes.POINTER(u32)]),
+            "shk_hip_program_set_graph_mode": (i32, [vp, i32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -271,6 +273,9 @@ class HipProgram:
         v = ctypes.c_uint32()
         check(self.lib, self.lib.shk_hip_program_step_count(self.handle, ctypes.byref(v)))
         return v.value
+
+    def set_graph_mode(self, enabled: bool) -> None:
+        check(self.lib, self.lib.shk_hip_program_set_graph_mode(self.handle, 1 if enabled else 0))
 
     def set_profiling(self, enabled: bool) -> None:
         check(self.lib, self.lib.shk_hip_program_set_profiling(self.handle, 1 if enabled else 0))

@@ -362,6 +362,14 @@ hipError_t launch_colsum(const float* x, float* out, int64_t R, int64_t N, int64
   return hipGetLastError();
 }
 
+hipError_t launch_colsum_finish(const double* partial, float* out, int64_t P, int64_t N,
+                                hipStream_t s) {
+  if (N <= 0) return hipSuccess;
+  hipLaunchKernelGGL(colsum_pass2, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s, partial,
+                     out, P, N, 1.0, 0);
+  return hipGetLastError();
+}
+
 hipError_t launch_row_reduce(const float* x, float* out, int64_t R, int64_t C, int kind,
                              hipStream_t s) {
   if (R <= 0) return hipSuccess;

@@ -240,6 +240,7 @@ gemm_f32_mfma(GemmParams p) {
     const int64_t col = n0 + wn * (NI * 32) + j * 32 + l32;
     const bool col_ok = col < p.N;
     const float bias = (p.bias != nullptr && col_ok) ? p.bias[col] : 0.f;
+    double csum = 0.0;  // fused column sum of this lane's stored values
     static_for<MI>([&](auto i) {
       const int64_t row0 = m0 + wm * (MI * 32) + i * 32 + half * 4;
       float* cptr = p.C + row0 * p.ldc + col;
@@ -258,10 +259,17 @@ gemm_f32_mfma(GemmParams p) {
           float* dst = cptr + off * p.ldc;
           if (p.accumulate) v = *dst + v;
           *dst = v;
+          csum += (double)v;
         }
       });
       __builtin_amdgcn_sched_barrier(0);
     });
+    if (p.colsum_partial != nullptr) {
+      // lanes l and l+32 hold the same column (different rows): one partial row per wave
+      csum += __shfl_xor(csum, 32, 64);
+      if (half == 0 && col_ok)
+        p.colsum_partial[((int64_t)tm * S::WGM + wm) * p.N + col] = csum;
+    }
   });
 }
 
@@ -308,10 +316,14 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(GemmParams p, int spli
   }
 }
 
+// Partial rows the last fused-column-sum launch on this thread wrote (ceil(M/BM) * BM/WM).
+thread_local int64_t g_colsum_rows = 0;
+
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB,
           int MINW = (BM / WM) * (BN / WN) >= 8 ? 2 : 1>
 hipError_t launch_cfg(const GemmParams& p, bool va, bool vb, hipStream_t s) {
   using S = GemmShape<BM, BN, BK, WM, WN>;
+  g_colsum_rows = ((p.M + BM - 1) / BM) * (BM / WM);
   const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
   const int64_t splits = p.kchunk > 0 ? (p.K + p.kchunk - 1) / p.kchunk : 1;
   dim3 grid((unsigned)tiles, (unsigned)splits), block(S::NT);
@@ -329,6 +341,7 @@ hipError_t launch_cfg(const GemmParams& p, bool va, bool vb, hipStream_t s) {
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int MINW>
 hipError_t launch_vec(const GemmParams& p, hipStream_t s) {
   using S = GemmShape<BM, BN, BK, WM, WN>;
+  g_colsum_rows = ((p.M + BM - 1) / BM) * (BM / WM);
   const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
   hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, TA, TB, true, true, MINW>), dim3((unsigned)tiles),
                      dim3(S::NT), 0, s, p);
@@ -391,15 +404,44 @@ int64_t splitk_chunk(int64_t K, int64_t s) {
 }
 }  // namespace
 
-int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0 || N <= 0 || K <= 1) return 0;
-  const int64_t s = splitk_slices(M, N, K);
-  if (s <= 1) return 0;
-  const int64_t slices = (K + splitk_chunk(K, s) - 1) / splitk_chunk(K, s);
-  return slices * M * N;
+int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K, bool colsum) {
+  if (M <= 0 || N <= 0) return 0;
+  int64_t floats = 0;
+  const int64_t s = K > 1 ? splitk_slices(M, N, K) : 1;
+  if (s > 1) {
+    const int64_t slices = (K + splitk_chunk(K, s) - 1) / splitk_chunk(K, s);
+    floats = slices * M * N;
+  }
+  if (colsum) {
+    // the fused path writes ceil(M/BM) * BM/WM binary64 rows, at most (M + 255) / 32 for every
+    // configuration (BM <= 256, WM >= 32); the split path's separate pass needs far fewer
+    floats = std::max<int64_t>(floats, 2 * ((M + 255) / 32) * N);
+  }
+  return floats;
 }
 
+hipError_t launch_gemm_core(const GemmParams& in, float* workspace, hipStream_t s);
+
+// Entry point: runs the GEMM and, when p.colsum is set, the column sum of the stored C -- fused
+// into the MFMA epilogue when the GEMM is not split along K, otherwise as a separate pass.
 hipError_t launch_gemm(const GemmParams& in, float* workspace, hipStream_t s) {
+  GemmParams p = in;
+  p.colsum_partial = nullptr;
+  if (p.colsum == nullptr || p.M <= 0 || p.N <= 0) return launch_gemm_core(p, workspace, s);
+  const bool split = p.K > 1 && splitk_slices(p.M, p.N, p.K) > 1;
+  if (p.K <= 1 || split) {
+    hipError_t e = launch_gemm_core(p, workspace, s);
+    if (e != hipSuccess) return e;
+    return launch_colsum(p.C, p.colsum, p.M, p.N, p.ldc, 1.0, 0,
+                         reinterpret_cast<double*>(workspace), s);
+  }
+  p.colsum_partial = reinterpret_cast<double*>(workspace);
+  hipError_t e = launch_gemm_core(p, workspace, s);
+  if (e != hipSuccess) return e;
+  return launch_colsum_finish(p.colsum_partial, p.colsum, g_colsum_rows, p.N, s);
+}
+
+hipError_t launch_gemm_core(const GemmParams& in, float* workspace, hipStream_t s) {
   GemmParams p = in;
   p.partial = nullptr;
   p.kchunk = 0;

@@ -35,11 +35,18 @@ struct GemmParams {
   // [y*kchunk, min(K, (y+1)*kchunk)) and writes raw partial sums to partial[y][M][N].
   float* partial;
   int64_t kchunk;
+  // Optional fused column sum of the stored C (SUM_TO_SHAPE for a bias gradient): colsum[N]
+  // receives the sum over all M rows; colsum_partial is launch_gemm's workspace.
+  float* colsum;
+  double* colsum_partial;
 };
 // `workspace` holds at least gemm_workspace_floats(M, N, K) floats (split-K partials); it may be
 // null when that is 0.
 hipError_t launch_gemm(const GemmParams& p, float* workspace, hipStream_t s);
-int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K);
+int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K, bool colsum = false);
+// Finishes a column sum from P partial rows (binary64, fixed order) into out[N].
+hipError_t launch_colsum_finish(const double* partial, float* out, int64_t P, int64_t N,
+                                hipStream_t s);
 
 // Column sums of X[R,N] (row stride ldx) into out[N]; out = (float)(sum * scale_num / scale_den)
 // with the sum accumulated in binary64. Used for SUM_TO_SHAPE (bias gradients) and MEAN.

@@ -267,7 +267,12 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
           !v.holds(s[2], span(M, N, ldc), DT_F32, "C") || !v.holds(s[3], N, DT_F32, "bias") ||
           !v.holds(s[4], span(M, N, ldaux), DT_F32, "aux") || !v.writable(s[2], "C"))
         return v.err;
-      need((uint64_t)((shk::gemm_workspace_floats(M, N, K) + 1) / 2));  // floats in double units
+      if (!v.slot_ok(s[5], true, "column sum") || !v.holds(s[5], N, DT_F32, "column sum") ||
+          !v.writable(s[5], "column sum"))
+        return v.err;
+      need((uint64_t)((shk::gemm_workspace_floats(M, N, K, s[5] >= 0) + 1) / 2));  // in doubles
+      // the separate column-sum pass of a split GEMM reuses the workspace for its partials
+      if (s[5] >= 0) need((uint64_t)shk::colsum_partial_doubles(M, N));
       return SHK_HIP_STATUS_OK;
     }
     case OP_COLSUM: {
@@ -483,6 +488,7 @@ hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipSt
       p.lda = a[3]; p.ldb = a[4]; p.ldc = a[5]; p.ldaux = a[6];
       p.transA = (int)a[7]; p.transB = (int)a[8];
       p.act = (int)a[9]; p.mode = (int)a[10]; p.accumulate = (int)a[11];
+      p.colsum = b.get<float>(s[5]);
       return shk::launch_gemm(p, reinterpret_cast<float*>(pr.scratch), stream);
     }
     case OP_COLSUM:

@@ -131,13 +131,14 @@ class ProgramBuilder:
     # ---- steps ----
     def gemm(self, A, B, C, M, N, K, *, trans_a=False, trans_b=False, lda=None, ldb=None,
              ldc=None, bias=None, act=None, aux=None, act_grad=False, ldaux=None,
-             accumulate=False) -> Step:
-        """C = op(A).op(B) (+bias, act) or C = act_grad(act, op(A).op(B), aux)."""
+             accumulate=False, colsum=None) -> Step:
+        """C = op(A).op(B) (+bias, act) or C = act_grad(act, op(A).op(B), aux); `colsum`
+        optionally receives the column sums of the stored C (a bias gradient)."""
         lda = lda if lda is not None else (M if trans_a else K)
         ldb = ldb if ldb is not None else (K if trans_b else N)
         ldc = ldc if ldc is not None else N
         ldaux = ldaux if ldaux is not None else N
-        return self._add(OP_GEMM, [A, B, C, bias, aux],
+        return self._add(OP_GEMM, [A, B, C, bias, aux, colsum],
                          [M, N, K, lda, ldb, ldc, ldaux, int(trans_a), int(trans_b), ACT[act],
                           1 if act_grad else 0, 1 if accumulate else 0])
 

@@ -28,6 +28,10 @@ from .program import ProgramBuilder, Slot
 
 ACTIVATIONS = (None, "relu", "tanh", "sigmoid")
 
+# Sum each hidden layer's bias gradient inside the epilogue of the dX GEMM that produces its
+# cotangent (instead of a separate column-sum pass over it).
+FUSE_BIAS_GRADIENT = True
+
 
 class GradientMode:
     """How one successful run uses its gradients (GradientMode.java):
@@ -258,18 +262,23 @@ def lower_training_step(spec: MlpSpec, batch: int, optimizer, *, label_dtype: st
             raise ValueError("cross-entropy consumes raw logits")
         pb.index_ce(acts[L], lay.y, lay.loss, batch, out_w, grad=cur)
     # backward
+    db_done = False  # the bias gradient of the current dZ was fused into the GEMM producing it
     for i in reversed(range(L)):
         l = spec.layers[i]
         # dW[out,in] = dZ^T . X   (PERMUTE of X^T.dZ absorbed)
         pb.gemm(cur, acts[i], gW[i], l.fan_out, l.fan_in, batch, trans_a=True)
-        if gb[i] is not None:
+        if gb[i] is not None and not db_done:
             pb.colsum(cur, gb[i], batch, l.fan_out)
+        db_done = False
         if i > 0:
             nxt = dz[1] if cur is dz[0] else dz[0]
             prev = spec.layers[i - 1]
-            # dZ_{i-1} = act_grad(dZ_i . W_i, Y_{i-1})
+            # dZ_{i-1} = act_grad(dZ_i . W_i, Y_{i-1}), with db_{i-1} = SUM_TO_SHAPE(dZ_{i-1})
+            # summed in the same epilogue
+            fuse = FUSE_BIAS_GRADIENT and gb[i - 1] is not None
             pb.gemm(cur, lay.weights[i], nxt, batch, l.fan_in, l.fan_out, aux=acts[i],
-                    act=prev.activation or "none", act_grad=True)
+                    act=prev.activation or "none", act_grad=True, colsum=gb[i - 1] if fuse else None)
+            db_done = fuse
             cur = nxt
     if mode != GradientMode.RESET_AND_STEP:
         # G = accumulator + G for every tensor, each candidate checked finite

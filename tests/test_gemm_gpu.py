@@ -128,3 +128,23 @@ def test_split_k_activation_gradient(ctx):
     y = oracle.activation("sigmoid", rng.standard_normal((M, N)).astype(np.float32))
     out = _gemm_case(ctx, dZ, W, M, N, K, False, False, aux=y, act="sigmoid", act_grad=True)
     assert np.array_equal(out, oracle.activation_grad("sigmoid", oracle.matmul(dZ, W), y))
+
+
+@pytest.mark.parametrize("shape", [(4096, 512, 256), (1000, 300, 64), (130, 72, 2048), (8192, 1024, 1024)])
+def test_fused_bias_gradient_column_sum(ctx, shape):
+    """GEMM with the activation-gradient epilogue and the SUM_TO_SHAPE of the stored result fused
+    (or, for split-K shapes, summed in a separate pass): column sums within 1 ulp of the exact sum."""
+    M, N, K = shape
+    rng = np.random.default_rng(M + N + K)
+    dZ = rng.standard_normal((M, K)).astype(np.float32)
+    W = rng.standard_normal((K, N)).astype(np.float32) * np.float32(0.05)
+    y = oracle.activation("relu", rng.standard_normal((M, N)).astype(np.float32))
+    pb = ProgramBuilder()
+    sa, sb, sy = pb.input(M * K), pb.input(K * N), pb.input(M * N)
+    sc, sd = pb.output(M * N), pb.output(N)
+    pb.gemm(sa, sb, sc, M, N, K, aux=sy, act="relu", act_grad=True, colsum=sd)
+    C, db = run_program(ctx, pb, [dZ, W, y], [sc, sd])
+    C = C.reshape(M, N)
+    np.testing.assert_array_max_ulp(db, oracle.colsum(C), maxulp=1)
+    ref = oracle.activation_grad("relu", oracle.matmul(dZ, W), y)
+    assert np.linalg.norm(C - ref) / np.linalg.norm(ref) < 1e-5

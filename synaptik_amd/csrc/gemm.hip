@@ -23,6 +23,7 @@
 //     block of output tiles: tiles that share A row-panels and B column-panels share an L2.
 #include "common.h"
 #include "kernels.h"
+#include "optim_math.h"
 #include <algorithm>
 #include <cstdlib>
 #include <type_traits>
@@ -53,6 +54,44 @@ struct GemmShape {
   static constexpr int PA = BM + 4;  // LDS pitch of the A tile (floats)
   static constexpr int PB = BN + 4;
 };
+
+// Fused optimizer update of one element from its gradient g (GemmParams::upd): the candidate
+// parameter and slots go to pn/mn/vn; returns false if an intermediate failed its check.
+struct UpdateCtx {
+  Coeffs k;
+  bool first;
+};
+__device__ __forceinline__ UpdateCtx update_ctx(const GemmUpdate& u) {
+  const int64_t completed = *u.completed_steps;
+  UpdateCtx c;
+  c.first = completed == 0;
+  c.k = Coeffs{1.0f, 1.0f, 1.0f, true};
+  if (u.kind != 0) c.k = adam_coeffs(u, completed + 1);
+  return c;
+}
+__device__ __forceinline__ bool update_element(const GemmUpdate& u, const UpdateCtx& c,
+                                               float pv, float g, float mv, float vv, int64_t e) {
+  float pc, mc, vc = 0.0f;
+  bool ok;
+  if (u.kind == 0) ok = sgd_element(u, c.first, pv, g, mv, pc, mc);
+  else ok = adam_element(u, c.k, pv, g, mv, vv, pc, mc, vc);
+  u.pn[e] = pc;
+  if (u.mn != nullptr) u.mn[e] = mc;
+  if (u.kind != 0) u.vn[e] = vc;
+  return ok;
+}
+// Flags a failed update in the program status word (one atomic per wave).
+__device__ __forceinline__ void update_flag(const GemmUpdate& u, const UpdateCtx& c, bool ok) {
+  const int bad = wave_or(ok ? 0 : 1);
+  if (bad && (threadIdx.x & 63) == 0)
+    atomicOr(u.status, c.k.ok ? (uint32_t)DEV_NON_FINITE : (uint32_t)DEV_NOT_POSITIVE);
+}
+__device__ __forceinline__ bool update_scalar(const GemmUpdate& u, const UpdateCtx& c, int64_t e,
+                                              float g) {
+  const float mv = u.m != nullptr ? u.m[e] : 0.0f;
+  const float vv = u.kind != 0 ? u.v[e] : 0.0f;
+  return update_element(u, c, u.p[e], g, mv, vv, e);
+}
 
 // Loads one BR x BK tile of an operand into registers and stores it into LDS as [k][r].
 //   KCONTIG: element (r, k) lives at ptr[r*ld + k]; otherwise at ptr[k*ld + r].
@@ -236,6 +275,45 @@ gemm_f32_mfma(GemmParams p) {
     });
     return;
   }
+  if (p.upd.pn != nullptr) {
+    // fused optimizer: per group of four rows, load the current parameters (and slots) of this
+    // lane first, then compute and store the candidates
+    const GemmUpdate& u = p.upd;
+    const UpdateCtx uc = update_ctx(u);
+    bool ok = uc.k.ok;
+    static_for<NI>([&](auto j) {
+      const int64_t col = n0 + wn * (NI * 32) + j * 32 + l32;
+      const bool col_ok = col < p.N;
+      static_for<MI>([&](auto i) {
+        const int64_t row0 = m0 + wm * (MI * 32) + i * 32 + half * 4;
+        const int64_t e0 = row0 * p.N + col;
+        // four rows at a time: loads of a group are issued together, few registers live
+        static_for<4>([&](auto q) {
+          constexpr int Q = decltype(q)::value;
+          float pv[4], mv[4], vv[4];
+          static_for<4>([&](auto r) {
+            constexpr int R = decltype(r)::value;
+            constexpr int off = Q * 8 + R;
+            pv[R] = 0.0f; mv[R] = 0.0f; vv[R] = 0.0f;
+            if (col_ok && row0 + off < p.M) {
+              pv[R] = u.p[e0 + off * p.N];
+              if (u.m != nullptr) mv[R] = u.m[e0 + off * p.N];
+              if (u.kind != 0) vv[R] = u.v[e0 + off * p.N];
+            }
+          });
+          static_for<4>([&](auto r) {
+            constexpr int R = decltype(r)::value;
+            constexpr int off = Q * 8 + R;
+            if (col_ok && row0 + off < p.M)
+              ok &= update_element(u, uc, pv[R], acc[i][j][Q * 4 + R], mv[R], vv[R], e0 + off * p.N);
+          });
+        });
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    });
+    update_flag(u, uc, ok);
+    return;
+  }
   static_for<NI>([&](auto j) {
     const int64_t col = n0 + wn * (NI * 32) + j * 32 + l32;
     const bool col_ok = col < p.N;
@@ -278,11 +356,22 @@ gemm_f32_mfma(GemmParams p) {
 // product; the MFMA path would add it to a +0 accumulator. Same epilogue as the MFMA kernel.
 __global__ void __launch_bounds__(256) gemm_k1_outer(GemmParams p) {
   const int64_t total = p.M * p.N;
+  const bool upd = p.upd.pn != nullptr;
+  UpdateCtx uc{};
+  bool ok = true;
+  if (upd) {
+    uc = update_ctx(p.upd);
+    ok = uc.k.ok;
+  }
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
     const int64_t row = e / p.N, col = e - row * p.N;
     const float a = p.A[row * (p.transA ? 1 : p.lda)];
     const float b = p.B[col * (p.transB ? p.ldb : 1)];
     float v = a * b;
+    if (upd) {
+      ok &= update_scalar(p.upd, uc, e, v);
+      continue;
+    }
     if (p.mode == 0) {
       if (p.bias != nullptr) v = v + p.bias[col];
       v = apply_act(p.act, v);
@@ -293,6 +382,7 @@ __global__ void __launch_bounds__(256) gemm_k1_outer(GemmParams p) {
     if (p.accumulate) v = *dst + v;
     *dst = v;
   }
+  if (upd) update_flag(p.upd, uc, ok);
 }
 
 // Split-K reduction: sums the slices of each output in slice order (a fixed binary32 order, so
@@ -300,10 +390,21 @@ __global__ void __launch_bounds__(256) gemm_k1_outer(GemmParams p) {
 __global__ void __launch_bounds__(256) gemm_splitk_reduce(GemmParams p, int splits) {
   const int64_t total = p.M * p.N;
   const int64_t plane = total;
+  const bool upd = p.upd.pn != nullptr;
+  UpdateCtx uc{};
+  bool ok = true;
+  if (upd) {
+    uc = update_ctx(p.upd);
+    ok = uc.k.ok;
+  }
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
     const int64_t row = e / p.N, col = e - row * p.N;
     float v = p.partial[e];
     for (int sidx = 1; sidx < splits; ++sidx) v = v + p.partial[sidx * plane + e];
+    if (upd) {
+      ok &= update_scalar(p.upd, uc, e, v);
+      continue;
+    }
     if (p.mode == 0) {
       if (p.bias != nullptr) v = v + p.bias[col];
       v = apply_act(p.act, v);
@@ -314,6 +415,7 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(GemmParams p, int spli
     if (p.accumulate) v = *dst + v;
     *dst = v;
   }
+  if (upd) update_flag(p.upd, uc, ok);
 }
 
 // Partial rows the last fused-column-sum launch on this thread wrote (ceil(M/BM) * BM/WM).

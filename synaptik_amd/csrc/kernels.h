@@ -21,6 +21,26 @@ enum DeviceStatus : uint32_t {
 //   mode 0 (forward):  C = act(acc + bias)             (bias optional, act in Act)
 //   mode 1 (backward): C = act_grad(act, acc, aux)       (aux = activation output y)
 //   accumulate != 0:   the epilogue value is added to the existing C (gradient accumulation).
+// Optimizer update fused into a GEMM epilogue that produces a weight gradient: the epilogue
+// stages the candidate parameter and slots exactly as the streaming optimizer's phase 2 (same
+// per-element arithmetic) from the freshly computed gradient, which is never stored. Enabled when
+// pn != nullptr; p, m, v, pn, mn, vn are row-major [M, N] like C. Field names match OptParams so
+// the shared element functions take either.
+struct GemmUpdate {
+  const float* p;
+  const float* m;
+  const float* v;
+  float* pn;
+  float* mn;
+  float* vn;
+  int kind;  // 0 SGD, 1 Adam, 2 AdamW
+  int nesterov, has_momentum_slot;
+  float lr, momentum, dampening, weight_decay;
+  float beta1, beta2, eps;
+  const int64_t* completed_steps;
+  uint32_t* status;
+};
+
 struct GemmParams {
   const float* A;
   const float* B;
@@ -39,6 +59,9 @@ struct GemmParams {
   // receives the sum over all M rows; colsum_partial is launch_gemm's workspace.
   float* colsum;
   double* colsum_partial;
+  // Optional fused optimizer update (C is then not written and may be null; requires ldc == N,
+  // mode 0, no bias, no activation, no accumulate, no column sum).
+  GemmUpdate upd;
 };
 // `workspace` holds at least gemm_workspace_floats(M, N, K) floats (split-K partials); it may be
 // null when that is 0.

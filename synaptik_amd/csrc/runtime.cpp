@@ -236,6 +236,46 @@ int64_t span(int64_t rows, int64_t cols, int64_t ld) {
   return (rows - 1) * ld + cols;
 }
 
+// GEMM whose epilogue stages an optimizer update from the gradient it computes (payload: one
+// tensor-table entry p, m, v, pn, mn, vn over the [M, N] result; slot 6: step counter). The
+// gradient itself is not stored, so C, bias, aux, column sum, activation and accumulation are
+// absent. Shapes and leading dimensions were checked by the caller.
+int32_t validate_gemm_update(Validator& v, size_t idx, const Step& st) {
+  const StepRecord& r = st.rec;
+  const int32_t* s = r.slot;
+  const int64_t* a = r.iarg;
+  const int64_t M = a[0], N = a[1], K = a[2], lda = a[3], ldb = a[4], ldc = a[5];
+  const int64_t tA = a[7], tB = a[8], kind = a[12];
+  if (st.payload.size() != sizeof(OptEntry))
+    return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: fused update needs one tensor entry", idx);
+  if (s[2] >= 0 || s[3] >= 0 || s[4] >= 0 || s[5] >= 0 || a[9] != 0 || a[10] != 0 || a[11] != 0 ||
+      ldc != N || kind < 0 || kind > 2)
+    return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED,
+                "step %zu: fused update GEMM takes no C, bias, aux, column sum, activation or accumulation", idx);
+  const OptEntry& e = *reinterpret_cast<const OptEntry*>(st.payload.data());
+  const bool adam = kind != 0;
+  if (e.n != M * N || e.g >= 0)
+    return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: fused update entry does not cover the result", idx);
+  if ((e.m >= 0) != (e.mn >= 0) || (e.v >= 0) != (e.vn >= 0))
+    return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: staged update lacks a candidate buffer", idx);
+  if (!v.slot_ok(s[0], false, "A") || !v.slot_ok(s[1], false, "B") ||
+      !v.slot_ok(s[6], false, "step counter") || !v.holds(s[6], 1, DT_I64, "step counter") ||
+      !v.holds(s[0], K == 0 ? 0 : (tA ? span(K, M, lda) : span(M, K, lda)), DT_F32, "A") ||
+      !v.holds(s[1], K == 0 ? 0 : (tB ? span(N, K, ldb) : span(K, N, ldb)), DT_F32, "B"))
+    return v.err;
+  if (!v.slot_ok(e.p, false, "param") || !v.slot_ok(e.m, !adam, "momentum") ||
+      !v.slot_ok(e.v, !adam, "second moment") || !v.slot_ok(e.pn, false, "param candidate") ||
+      !v.slot_ok(e.mn, true, "momentum candidate") || !v.slot_ok(e.vn, true, "second moment candidate") ||
+      !v.holds(e.p, e.n, DT_F32, "param") || !v.holds(e.m, e.n, DT_F32, "momentum") ||
+      !v.holds(e.v, e.n, DT_F32, "second moment") || !v.holds(e.pn, e.n, DT_F32, "param candidate") ||
+      !v.holds(e.mn, e.n, DT_F32, "momentum candidate") ||
+      !v.holds(e.vn, e.n, DT_F32, "second moment candidate") ||
+      !v.writable(e.pn, "param candidate") || !v.writable(e.mn, "momentum candidate") ||
+      !v.writable(e.vn, "second moment candidate"))
+    return v.err;
+  return SHK_HIP_STATUS_OK;
+}
+
 int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const Step& st,
                       uint64_t* scratch_doubles) {
   Validator v{slots, idx};
@@ -259,6 +299,10 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
         return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: GEMM leading dimension too small", idx);
       if (mode == 1 && s[4] < 0)
         return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: activation gradient needs aux", idx);
+      if (!st.payload.empty()) {
+        need((uint64_t)((shk::gemm_workspace_floats(M, N, K, false) + 1) / 2));  // in doubles
+        return validate_gemm_update(v, idx, st);
+      }
       if (!v.slot_ok(s[0], false, "A") || !v.slot_ok(s[1], false, "B") || !v.slot_ok(s[2], false, "C") ||
           !v.slot_ok(s[3], true, "bias") || !v.slot_ok(s[4], true, "aux"))
         return v.err;
@@ -489,6 +533,21 @@ hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipSt
       p.transA = (int)a[7]; p.transB = (int)a[8];
       p.act = (int)a[9]; p.mode = (int)a[10]; p.accumulate = (int)a[11];
       p.colsum = b.get<float>(s[5]);
+      if (!st.payload.empty()) {
+        const OptEntry& e = *reinterpret_cast<const OptEntry*>(st.payload.data());
+        shk::GemmUpdate& u = p.upd;
+        u.p = b.get<const float>(e.p);
+        u.m = b.get<const float>(e.m);
+        u.v = b.get<const float>(e.v);
+        u.pn = b.get<float>(e.pn);
+        u.mn = b.get<float>(e.mn);
+        u.vn = b.get<float>(e.vn);
+        u.kind = (int)a[12]; u.nesterov = (int)a[13]; u.has_momentum_slot = (int)a[14];
+        u.lr = r.farg[0]; u.momentum = r.farg[1]; u.dampening = r.farg[2]; u.weight_decay = r.farg[3];
+        u.beta1 = r.farg[4]; u.beta2 = r.farg[5]; u.eps = r.farg[6];
+        u.completed_steps = b.get<const int64_t>(s[6]);
+        u.status = pr.status;
+      }
       return shk::launch_gemm(p, reinterpret_cast<float*>(pr.scratch), stream);
     }
     case OP_COLSUM:

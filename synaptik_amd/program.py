@@ -142,6 +142,25 @@ class ProgramBuilder:
                          [M, N, K, lda, ldb, ldc, ldaux, int(trans_a), int(trans_b), ACT[act],
                           1 if act_grad else 0, 1 if accumulate else 0])
 
+    def gemm_update(self, A, B, M, N, K, counter, tensor, *, kind: str, trans_a=False,
+                    trans_b=False, lda=None, ldb=None, lr: float, momentum=0.0, dampening=0.0,
+                    weight_decay=0.0, nesterov=False, has_momentum_slot=False, beta1=0.9,
+                    beta2=0.999, eps=1e-8) -> Step:
+        """G = op(A).op(B) consumed by a staged optimizer update in the GEMM epilogue.
+
+        tensor = (param, m, v, param_next, m_next, v_next) over the row-major [M, N] result; the
+        candidates are written exactly as OPTIMIZER phase 2 would from G, which is not stored."""
+        k = {"sgd": 0, "adam": 1, "adamw": 2}[kind]
+        lda = lda if lda is not None else (M if trans_a else K)
+        ldb = ldb if ldb is not None else (K if trans_b else N)
+        p, m, v, pn, mn, vn = tensor
+        payload = struct.pack("<iiiiiiiiq", _sid(p), -1, _sid(m), _sid(v), _sid(pn), _sid(mn),
+                              _sid(vn), 0, int(M) * int(N))
+        return self._add(OP_GEMM, [A, B, None, None, None, None, counter],
+                         [M, N, K, lda, ldb, N, N, int(trans_a), int(trans_b), 0, 0, 0, k,
+                          int(nesterov), int(has_momentum_slot)],
+                         [lr, momentum, dampening, weight_decay, beta1, beta2, eps], payload)
+
     def colsum(self, X, out, R, N, *, ldx=None, mean=False, accumulate=False) -> Step:
         return self._add(OP_COLSUM, [X, out], [R, N, ldx if ldx is not None else N,
                                                int(accumulate), int(mean)])

@@ -31,6 +31,9 @@ ACTIVATIONS = (None, "relu", "tanh", "sigmoid")
 # Sum each hidden layer's bias gradient inside the epilogue of the dX GEMM that produces its
 # cotangent (instead of a separate column-sum pass over it).
 FUSE_BIAS_GRADIENT = True
+# In RESET_AND_STEP runs, stage each weight's optimizer update in the epilogue of the GEMM that
+# computes its gradient (the gradient is never stored and the weights skip the streaming pass).
+FUSE_OPTIMIZER = True
 
 
 class GradientMode:
@@ -200,8 +203,9 @@ def lower_training_step(spec: MlpSpec, batch: int, optimizer, *, label_dtype: st
     int64), x [batch, in], y ([batch, out] f32 for MSE; [batch] int for CE).
     Output: objective [1].
 
-    The update is one streaming pass that reads the current set and writes the candidate set; the
-    caller adopts the candidate set only when the run succeeds. Every mode is transactional: a
+    The update reads the current set and writes the candidate set: for RESET_AND_STEP each
+    weight's update runs in the epilogue of its gradient GEMM (FUSE_OPTIMIZER), the rest is one
+    streaming pass after the backward sweep. The caller adopts the candidate set only when the run succeeds. Every mode is transactional: a
     non-finite accumulated candidate or optimizer intermediate leaves the current parameters,
     slots, accumulators and the counter unchanged.
     """
@@ -261,12 +265,29 @@ def lower_training_step(spec: MlpSpec, batch: int, optimizer, *, label_dtype: st
         if spec.layers[-1].activation is not None:
             raise ValueError("cross-entropy consumes raw logits")
         pb.index_ce(acts[L], lay.y, lay.loss, batch, out_w, grad=cur)
+    common = {}
+    if kind == "sgd":
+        common = dict(lr=optimizer.learning_rate, momentum=optimizer.momentum,
+                      dampening=optimizer.dampening, weight_decay=optimizer.weight_decay,
+                      nesterov=optimizer.nesterov, has_momentum_slot=has_first)
+    else:
+        common = dict(lr=optimizer.learning_rate, beta1=optimizer.beta1, beta2=optimizer.beta2,
+                      eps=optimizer.epsilon, weight_decay=optimizer.weight_decay)
+    fuse_update = FUSE_OPTIMIZER and mode == GradientMode.RESET_AND_STEP
     # backward
     db_done = False  # the bias gradient of the current dZ was fused into the GEMM producing it
     for i in reversed(range(L)):
         l = spec.layers[i]
         # dW[out,in] = dZ^T . X   (PERMUTE of X^T.dZ absorbed)
-        pb.gemm(cur, acts[i], gW[i], l.fan_out, l.fan_in, batch, trans_a=True)
+        if fuse_update:
+            pb.gemm_update(cur, acts[i], l.fan_out, l.fan_in, batch, lay.counter,
+                           (lay.weights[i], lay.first[i] if has_first else None,
+                            lay.second[i] if lay.second else None, lay.weights_next[i],
+                            lay.first_next[i] if has_first else None,
+                            lay.second_next[i] if lay.second else None),
+                           kind=kind, trans_a=True, **common)
+        else:
+            pb.gemm(cur, acts[i], gW[i], l.fan_out, l.fan_in, batch, trans_a=True)
         if gb[i] is not None and not db_done:
             pb.colsum(cur, gb[i], batch, l.fan_out)
         db_done = False
@@ -293,18 +314,12 @@ def lower_training_step(spec: MlpSpec, batch: int, optimizer, *, label_dtype: st
     params_next = lay.weights_next + [b for b in lay.biases_next if b is not None]
     entries = []
     for j, p in enumerate(params):
+        if fuse_update and j < L:
+            continue  # weight updated in its gradient GEMM's epilogue
         entries.append((p, lay.grads[j], lay.first[j] if has_first else None,
                         lay.second[j] if lay.second else None, params_next[j],
                         lay.first_next[j] if has_first else None,
                         lay.second_next[j] if lay.second else None, p.count))
-    common = {}
-    if kind == "sgd":
-        common = dict(lr=optimizer.learning_rate, momentum=optimizer.momentum,
-                      dampening=optimizer.dampening, weight_decay=optimizer.weight_decay,
-                      nesterov=optimizer.nesterov, has_momentum_slot=has_first)
-    else:
-        common = dict(lr=optimizer.learning_rate, beta1=optimizer.beta1, beta2=optimizer.beta2,
-                      eps=optimizer.epsilon, weight_decay=optimizer.weight_decay)
     for i in range(0, len(entries), 16):
         pb.optimizer(lay.counter, entries[i:i + 16], kind=kind, phase=2, **common)
     if uses_acc:

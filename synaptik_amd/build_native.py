@@ -19,7 +19,9 @@ OUT_DIR = PKG / "_build"
 LIBRARY = PKG / "libsynaptik_hip.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["gemm.hip", "elementwise.hip", "softmax_loss.hip", "optim.hip", "runtime.cpp"]
+# the per-layout GEMM units are the slowest to compile and go first
+SOURCES = ["gemm_nn.hip", "gemm_nt.hip", "gemm_tn.hip", "gemm_tt.hip", "gemm.hip",
+           "elementwise.hip", "softmax_loss.hip", "optim.hip", "runtime.cpp"]
 
 COMMON_FLAGS = [
     "--offload-arch=gfx950",

@@ -203,8 +203,40 @@ def secondary(ctx, reps: int = 5, cpu: bool = True) -> dict:
                                  "ms_per_step": round(wall / 50 * 1e3, 4),
                                  "objective_first": first, "objective_last": float(sess.objective())}
     sess.close()
+    # Canonical host publication of the MLP-4096 output [4096, 4096] FLOAT32: dense and a
+    # transposed view, device packing + one device-to-host copy into pageable host memory
+    from synaptik_amd.backend import HipBackendIntegration, TensorDescriptor
+    integ = HipBackendIntegration.open(0)
+    data = rng.standard_normal((BATCH, WIDTH), dtype=np.float32)
+    buf = integ.borrow("FLOAT32", data)
+    pub = {}
+    for name, desc in (("dense", TensorDescriptor("FLOAT32", (BATCH, WIDTH))),
+                       ("transposed", TensorDescriptor("FLOAT32", (WIDTH, BATCH), (1, WIDTH)))):
+        integ.copy_to_canonical_host_bytes(buf, desc, data.nbytes)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            integ.copy_to_canonical_host_bytes(buf, desc, data.nbytes)
+        ms = (time.perf_counter() - t0) / reps * 1e3
+        pub[name] = {"ms": round(ms, 3), "host_GBps": round(data.nbytes / ms / 1e6, 1)}
+    buf.download(np.float32)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        buf.download(np.float32)
+    raw_ms = (time.perf_counter() - t0) / reps * 1e3
+    out["canonical_publication"] = {"shape": [BATCH, WIDTH], "dtype": "FLOAT32", **pub,
+                                    "raw_download_ms": round(raw_ms, 3)}
+    buf.close()
+    integ.close()
     if cpu:
         add_cpu_baselines(out)
+        from oracle import oracle
+        raw = data[:256].tobytes()
+        t0 = time.perf_counter()
+        oracle.canonical_bytes(raw, 4, (256, WIDTH))
+        dt = time.perf_counter() - t0
+        out["canonical_publication"]["cpu_baseline"] = {
+            "ms_full": round(dt * BATCH / 256 * 1e3, 1), "cores": 1, "kind": "port",
+            "sample": f"oracle per-element packing of 256 of 4096 rows ({dt:.3f} s), scaled x16"}
     return out
 
 
@@ -269,6 +301,9 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true", help="skip the C2/C3/C5 lines")
     ap.add_argument("--probe", action="store_true",
                     help="counter probe: 3 launches each of one 4096^3 NT GEMM and a 256 MiB copy")
+    ap.add_argument("--secondary-only", action="store_true",
+                    help="only the C2/C3/C5 and publication lines, without CPU baselines "
+                         "(for kernel profiles)")
     args = ap.parse_args()
     if args.probe:
         return probe()
@@ -279,6 +314,10 @@ def main() -> int:
 
     from synaptik_amd.native import HipContext
     ctx = HipContext(0)
+    if args.secondary_only:
+        print(json.dumps({"secondary": secondary(ctx, cpu=False)}), flush=True)
+        ctx.close()
+        return 0
     info = ctx.device_info()
     spec, Ws, bs, sess, x, y = build_session(ctx)
     print(f"[bench] device {info}", file=sys.stderr, flush=True)

@@ -80,6 +80,23 @@ int32_t shk_hip_buffer_release(void* buffer);
 int32_t shk_hip_buffer_upload(void* buffer, uint64_t offset, const void* source, uint64_t byte_count);
 int32_t shk_hip_buffer_download(void* buffer, uint64_t offset, void* destination, uint64_t byte_count);
 int32_t shk_hip_buffer_device_pointer(void* buffer, void** out_pointer);
+/* Canonical host publication. Replaces the host-side packing of
+ * MetalBackendRuntime.copyToCanonicalHostBytes (modules/backend/metal/src/main/java/io/github/
+ * pho001/synaptik/backend/metal/MetalBackendRuntime.java:304-424, HostTensorValue.java:18):
+ * writes the rank-`rank` view of `buffer` (dims; element strides, NULL = dense row-major;
+ * storage_offset in elements) to destination as dense row-major bytes, every multi-byte element
+ * big-endian with its raw bits kept. element_width is 1, 2, 4 or 8; boolean != 0 marks BOOL
+ * (one byte per element), whose elements must be 0 or 1 (otherwise INVALID_ARGUMENT and nothing
+ * is written). Checks, in the reference's order: payload bytes > maximum_bytes
+ * (INVALID_ARGUMENT), payload > destination_capacity, referenced span beyond the buffer,
+ * rank > 16, negative extents / strides / offset (all INVALID_ARGUMENT). An empty view returns
+ * OK without device work. The packing is one device pass into a context-owned staging buffer
+ * followed by one device-to-host copy; the call is synchronous. */
+int32_t shk_hip_buffer_download_canonical(void* buffer, uint32_t element_width, int32_t boolean,
+                                          uint32_t rank, const int64_t* dims,
+                                          const int64_t* strides, int64_t storage_offset,
+                                          void* destination, uint64_t destination_capacity,
+                                          uint64_t maximum_bytes);
 
 /* Programs: an op-list image (the HIP analogue of the Metal graph image decoded by
  * synaptik_metal_mpsgraph_executable_create, synaptik_metal_foundation.m:8573). The program

@@ -68,6 +68,8 @@ def lib():
                                      i32, i64]),
             "shko_adam_stage": (i32, [F32P, F32P, F32P, F32P, F32P, F32P, F32P, i64, f32, f32,
                                       f32, f32, f32, i32, i64]),
+            "shko_canonical_bytes": (i32, [ctypes.c_void_p, ctypes.c_uint64, i32, i32, i32, I64P,
+                                           I64P, i64, ctypes.c_void_p]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -237,6 +239,28 @@ def adam_stage(p, g, m, v, *, lr, beta1, beta2, eps, weight_decay=0.0, decoupled
 
 
 # ---- MLP training step ----
+def canonical_bytes(raw: bytes, width: int, shape, strides=None, offset: int = 0,
+                    boolean: bool = False) -> bytes:
+    """Canonical big-endian row-major bytes of a view over little-endian storage `raw`
+    (MetalBackendRuntime.java:360-398,489-499). Raises ValueError for a non-canonical BOOL byte
+    or a view outside the storage."""
+    shape = tuple(int(d) for d in shape)
+    count = int(np.prod(shape, dtype=np.int64)) if shape else 1
+    w = 1 if boolean else int(width)
+    src = np.frombuffer(bytes(raw), dtype=np.uint8)
+    dst = np.zeros(max(1, count * w), np.uint8)
+    dims = (ctypes.c_int64 * max(1, len(shape)))(*shape)
+    st = None if strides is None else (ctypes.c_int64 * max(1, len(shape)))(*strides)
+    rc = lib().shko_canonical_bytes(src.ctypes.data if src.size else None, src.size, w,
+                                    1 if boolean else 0, len(shape), dims, st, int(offset),
+                                    dst.ctypes.data)
+    if rc == 1:
+        raise ValueError("BOOL source contains a non-canonical byte")
+    if rc == 2:
+        raise ValueError("view lies outside the storage")
+    return dst.tobytes()[:count * w]
+
+
 class OracleMLP:
     """Fully-connected network with per-layer activations; weights W[out,in], biases [out].
 

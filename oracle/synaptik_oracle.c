@@ -572,3 +572,36 @@ int shko_adam_stage(const float* p, const float* g, const float* m, const float*
   }
   return 0;
 }
+
+/* Canonical host publication (MetalBackendRuntime.copyToCanonicalHostBytes,
+ * MetalBackendRuntime.java:360-398, with storageElementIndex :489-499): for every row-major
+ * ordinal, the storage element is offset + sum(coordinate_a * stride_a) with the coordinates
+ * peeled from the last axis; its `width` bytes are written in reverse (little-endian host ->
+ * big-endian) order; BOOL elements must be 0 or 1. strides == NULL means dense row-major.
+ * Returns 0, 1 for a non-canonical BOOL byte, 2 for a span outside src (nothing is promised
+ * about dst after a non-zero return). */
+int shko_canonical_bytes(const uint8_t* src, uint64_t src_bytes, int width, int boolean,
+                         int rank, const int64_t* dims, const int64_t* strides, int64_t offset,
+                         uint8_t* dst) {
+  int64_t elements = 1;
+  for (int a = 0; a < rank; ++a) elements *= dims[a];
+  for (int64_t ordinal = 0; ordinal < elements; ++ordinal) {
+    int64_t remaining = ordinal, storage = offset, dense_stride = 1;
+    for (int a = rank - 1; a >= 0; --a) {
+      const int64_t coordinate = remaining % dims[a];
+      remaining /= dims[a];
+      const int64_t stride = strides != NULL ? strides[a] : dense_stride;
+      storage += coordinate * stride;
+      dense_stride *= dims[a];
+    }
+    const uint64_t at = (uint64_t)storage * (uint64_t)width;
+    if (at + (uint64_t)width > src_bytes) return 2;
+    if (boolean) {
+      if (src[at] != 0 && src[at] != 1) return 1;
+      dst[ordinal] = src[at];
+      continue;
+    }
+    for (int k = 0; k < width; ++k) dst[ordinal * width + k] = src[at + (uint64_t)(width - 1 - k)];
+  }
+  return 0;
+}

@@ -34,6 +34,9 @@ int shko_sgd_stage(const float* p, const float* g, const float* m, float* p_out,
 int shko_adam_stage(const float* p, const float* g, const float* m, const float* v, float* p_out,
                     float* m_out, float* v_out, int64_t n, float lr, float b1, float b2, float eps,
                     float decay, int decoupled, int64_t completed_steps);
+int shko_canonical_bytes(const uint8_t* src, uint64_t src_bytes, int width, int boolean,
+                         int rank, const int64_t* dims, const int64_t* strides, int64_t offset,
+                         uint8_t* dst);
 #ifdef __cplusplus
 }
 #endif

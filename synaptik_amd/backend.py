@@ -47,6 +47,11 @@ ELEMENTWISE_BINARY = {"ADD": "add", "SUB": "sub", "MUL": "mul", "DIV": "div", "M
                       "GREATER_THAN": "gt"}
 ACTIVATIONS = {"RELU": "relu", "TANH": "tanh", "SIGMOID": "sigmoid"}
 DTYPE_SLOT = {"FLOAT32": "f32", "INT32": "i32", "INT64": "i64", "BOOL": "f32"}
+# Storage widths of the publishable types (DataType.byteWidth); FP8 is rejected like Metal does
+# (MetalBackendRuntime.requireStorageType).
+STORAGE_WIDTH = {"FLOAT64": 8, "FLOAT32": 4, "BFLOAT16": 2, "FLOAT16": 2, "INT64": 8, "INT32": 4,
+                 "BOOL": 1}
+UNSUPPORTED_STORAGE = ("FLOAT8_E4M3", "FLOAT8_E5M2")
 
 
 class UnsupportedPartition(ValueError):
@@ -55,8 +60,12 @@ class UnsupportedPartition(ValueError):
 
 @dataclass(frozen=True)
 class TensorDescriptor:
+    """Logical type and shape; `strides` / `storage_offset` (element units) describe a view's
+    storage layout (None: dense row-major), as LayoutDescriptor does in the reference."""
     dtype: str
     shape: tuple
+    strides: Optional[tuple] = None
+    storage_offset: int = 0
 
     @property
     def count(self) -> int:
@@ -290,6 +299,51 @@ class HipBackendIntegration:
 
     def prepare(self, part: Partition) -> HipPreparedExecutable:
         return self.finalizer.finalize_partition(self.preparer.analyze(part))
+
+    def _require_open(self):
+        if not self.context.handle:
+            raise RuntimeError("HIP device context is closed")  # IllegalStateException
+
+    @staticmethod
+    def _require_storage_type(dtype: str) -> int:
+        if dtype in UNSUPPORTED_STORAGE or dtype not in STORAGE_WIDTH:
+            raise ValueError(f"HIP does not support storage type {dtype}")
+        return STORAGE_WIDTH[dtype]
+
+    def borrow(self, dtype: str, storage: np.ndarray) -> HipBuffer:
+        """Uploads caller host storage into a new device buffer owned by the caller
+        (MetalBackendRuntime.borrow, MetalBackendRuntime.java:173-200): raw storage bytes, BOOL
+        not interpreted here; FP8 rejected before any allocation."""
+        self._require_storage_type(dtype)
+        self._require_open()
+        raw = np.ascontiguousarray(storage).view(np.uint8).reshape(-1)
+        buf = HipBuffer(self.context, raw.nbytes)
+        try:
+            if raw.nbytes:
+                buf.upload(raw)
+        except BaseException:
+            buf.close()
+            raise
+        return buf
+
+    def copy_to_canonical_host_bytes(self, buffer: HipBuffer, descriptor: TensorDescriptor,
+                                     maximum_bytes: int) -> memoryview:
+        """Canonical dense row-major big-endian bytes of a publication
+        (MetalBackendRuntime.copyToCanonicalHostBytes, MetalBackendRuntime.java:304-424;
+        HostTensorValue.java:18): raw bits kept, BOOL elements must be 0 or 1, strided views
+        gathered in row-major order. Packing runs on the device."""
+        if buffer is None or descriptor is None:
+            raise TypeError("buffer and descriptor must not be None")  # NullPointerException
+        width = self._require_storage_type(descriptor.dtype)
+        self._require_open()
+        if maximum_bytes < 0:
+            raise ValueError("maximumBytes must be non-negative")
+        if buffer.ctx is not self.context or not buffer.handle:
+            raise ValueError("representation must be a live readable buffer owned by this HIP integration")
+        return buffer.download_canonical(width, descriptor.shape, descriptor.strides,
+                                         descriptor.storage_offset,
+                                         boolean=descriptor.dtype == "BOOL",
+                                         maximum_bytes=maximum_bytes)
 
     def close(self):
         self.context.close()

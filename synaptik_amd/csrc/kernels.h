@@ -13,6 +13,7 @@ enum DeviceStatus : uint32_t {
   DEV_NON_FINITE = 1,       // an optimizer intermediate or candidate was not finite
   DEV_INDEX_OUT_OF_BOUNDS = 2,  // a categorical target index lies outside the class extent
   DEV_NOT_POSITIVE = 4,     // an adaptive bias correction or denominator was not positive
+  DEV_INVALID_BOOL = 8,     // a published BOOL element held a byte other than 0 or 1
 };
 
 // C[M,N] = op(A)[M,K] . op(B)[K,N] with a fused epilogue.
@@ -167,6 +168,21 @@ hipError_t launch_step_commit(int64_t* counter, const uint32_t* status, hipStrea
 hipError_t launch_fill(float* x, int64_t n, float value, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* x, int64_t n, uint32_t value, hipStream_t s);
 hipError_t launch_copy(const float* src, float* dst, int64_t n, hipStream_t s);
+// Canonical publication geometry of a strided view (element units, row-major ordinals).
+constexpr int CANONICAL_MAX_RANK = 16;
+struct CanonicalGeometry {
+  int64_t dims[CANONICAL_MAX_RANK];
+  int64_t strides[CANONICAL_MAX_RANK];
+  int64_t offset;
+  int32_t rank;
+};
+// Packs `elements` elements of `width` bytes (1, 2, 4, 8) from src into dense big-endian bytes at
+// dst; g == nullptr means src is dense from element 0 (src and dst 16-byte aligned). boolean: the
+// elements are BOOL bytes, any value other than 0 / 1 ORs DEV_INVALID_BOOL into *status.
+hipError_t launch_canonical_pack(const void* src, void* dst, int64_t elements, int width,
+                                 int boolean, const CanonicalGeometry* g, uint32_t* status,
+                                 hipStream_t s);
+
 // Y[C,R] = X[R,C]^T
 hipError_t launch_transpose(const float* x, float* y, int64_t R, int64_t C, hipStream_t s);
 

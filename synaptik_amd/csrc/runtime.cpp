@@ -61,6 +61,10 @@ struct Context {
   int device = 0;
   hipStream_t stream = nullptr;
   uint32_t* host_status = nullptr;  // pinned
+  // Device staging of canonical publications: a 256-byte status block, then the packed bytes.
+  // Grown on demand, guarded by `mutex`, freed with the context.
+  uint8_t* pub_staging = nullptr;
+  uint64_t pub_staging_bytes = 0;
   std::mutex mutex;
   std::atomic<int64_t> refs{1};
   std::atomic<bool> released{false};
@@ -72,6 +76,7 @@ void context_unref(Context* c) {
   (void)hipStreamSynchronize(c->stream);
   (void)hipStreamDestroy(c->stream);
   (void)hipHostFree(c->host_status);
+  if (c->pub_staging != nullptr) (void)hipFree(c->pub_staging);
   c->magic = 0;
   delete c;
 }
@@ -785,6 +790,131 @@ int32_t shk_hip_buffer_download(void* buffer, uint64_t offset, void* destination
   if (hipMemcpyAsync(destination, static_cast<const char*>(b->ptr) + offset, byte_count,
                      hipMemcpyDeviceToHost, b->ctx->stream) != hipSuccess ||
       hipStreamSynchronize(b->ctx->stream) != hipSuccess)
+    return fail(SHK_HIP_STATUS_COPY_FAILED, "device-to-host copy failed");
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_buffer_download_canonical(void* buffer, uint32_t element_width, int32_t boolean,
+                                          uint32_t rank, const int64_t* dims,
+                                          const int64_t* strides, int64_t storage_offset,
+                                          void* destination, uint64_t destination_capacity,
+                                          uint64_t maximum_bytes) {
+  // Argument order and checks follow MetalBackendRuntime.copyToCanonicalHostBytes
+  // (MetalBackendRuntime.java:304-357): payload limit, then the referenced storage span.
+  Buffer* b = checked<Buffer, kBufferMagic>(buffer);
+  if (b == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a buffer handle");
+  if (b->ctx->released.load()) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "context is released");
+  if (boolean) element_width = 1;
+  if (element_width != 1 && element_width != 2 && element_width != 4 && element_width != 8)
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "element width must be 1, 2, 4 or 8");
+  if (rank > (uint32_t)shk::CANONICAL_MAX_RANK || (rank > 0 && dims == nullptr))
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "rank must be 0..16 with dimensions");
+  if (storage_offset < 0) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "negative storage offset");
+  // element count and referenced span (LayoutGeometry.referencedElementSpan), overflow-checked
+  uint64_t elements = 1, greatest = (uint64_t)storage_offset;
+  bool empty = false;
+  for (uint32_t a = 0; a < rank; ++a) {
+    if (dims[a] < 0) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "negative dimension");
+    if (strides != nullptr && strides[a] < 0)
+      return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "negative stride");
+    if (dims[a] == 0) empty = true;
+  }
+  for (uint32_t a = 0; a < rank && !empty; ++a) {
+    if (__builtin_mul_overflow(elements, (uint64_t)dims[a], &elements))
+      return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "element count overflows");
+  }
+  if (empty) elements = 0;
+  uint64_t byte_count;
+  if (__builtin_mul_overflow(elements, (uint64_t)element_width, &byte_count))
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "byte count overflows");
+  if (byte_count > maximum_bytes)
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT,
+                "canonical payload exceeds maximumBytes: required=%llu, maximum=%llu",
+                (unsigned long long)byte_count, (unsigned long long)maximum_bytes);
+  if (byte_count > destination_capacity || (destination == nullptr && byte_count != 0))
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "destination is smaller than the payload");
+  uint64_t span = 0;  // referenced elements
+  if (!empty) {
+    if (strides == nullptr) {
+      if (__builtin_add_overflow(greatest, elements, &span))
+        return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "span overflows");
+    } else {
+      for (uint32_t a = 0; a < rank; ++a) {
+        uint64_t ext;
+        if (__builtin_mul_overflow((uint64_t)(dims[a] - 1), (uint64_t)strides[a], &ext) ||
+            __builtin_add_overflow(greatest, ext, &greatest))
+          return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "span overflows");
+      }
+      span = greatest + 1;
+    }
+  }
+  uint64_t span_bytes;
+  if (__builtin_mul_overflow(span, (uint64_t)element_width, &span_bytes) || span_bytes > b->bytes)
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "buffer is smaller than the descriptor's span");
+  if (elements == 0) return SHK_HIP_STATUS_OK;
+
+  // Dense from element 0: no gather. Otherwise the strided kernel with the view's geometry.
+  bool dense = storage_offset == 0;
+  if (strides != nullptr) {
+    int64_t expect = 1;
+    for (int a = (int)rank - 1; a >= 0 && dense; --a) {
+      if (dims[a] != 1 && strides[a] != expect) dense = false;
+      expect *= dims[a];
+    }
+  }
+  shk::CanonicalGeometry g{};
+  if (!dense) {
+    g.rank = (int32_t)rank;
+    g.offset = storage_offset;
+    for (uint32_t a = 0; a < rank; ++a) {
+      g.dims[a] = dims[a];
+      g.strides[a] = strides != nullptr ? strides[a] : 0;
+    }
+    if (strides == nullptr) {  // dense row-major strides from a non-zero offset
+      int64_t st = 1;
+      for (int a = (int)rank - 1; a >= 0; --a) { g.strides[a] = st; st *= dims[a]; }
+    }
+  }
+  Context* c = b->ctx;
+  std::lock_guard<std::mutex> lock(c->mutex);
+  HIP_TRY(hipSetDevice(c->device));
+  // raw little-endian single bytes need no device pass
+  if (dense && element_width == 1 && !boolean) {
+    if (hipMemcpyAsync(destination, b->ptr, byte_count, hipMemcpyDeviceToHost, c->stream) !=
+            hipSuccess ||
+        hipStreamSynchronize(c->stream) != hipSuccess)
+      return fail(SHK_HIP_STATUS_COPY_FAILED, "device-to-host copy failed");
+    return SHK_HIP_STATUS_OK;
+  }
+  const uint64_t need = 256 + ((byte_count + 255) / 256) * 256;
+  if (c->pub_staging_bytes < need) {
+    if (c->pub_staging != nullptr) {
+      HIP_TRY(hipStreamSynchronize(c->stream));
+      (void)hipFree(c->pub_staging);
+      c->pub_staging = nullptr;
+      c->pub_staging_bytes = 0;
+    }
+    if (hipMalloc((void**)&c->pub_staging, need) != hipSuccess) {
+      c->pub_staging = nullptr;
+      return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "publication staging of %llu bytes failed",
+                  (unsigned long long)need);
+    }
+    c->pub_staging_bytes = need;
+  }
+  uint32_t* status = reinterpret_cast<uint32_t*>(c->pub_staging);
+  uint8_t* packed = c->pub_staging + 256;
+  HIP_TRY(shk::launch_fill_u32(status, 1, 0u, c->stream));
+  HIP_TRY(shk::launch_canonical_pack(b->ptr, packed, (int64_t)elements, (int)element_width,
+                                     boolean, dense ? nullptr : &g, status, c->stream));
+  if (boolean) {
+    HIP_TRY(hipMemcpyAsync(c->host_status, status, 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (*c->host_status & shk::DEV_INVALID_BOOL)
+      return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "BOOL source contains a non-canonical byte");
+  }
+  if (hipMemcpyAsync(destination, packed, byte_count, hipMemcpyDeviceToHost, c->stream) !=
+          hipSuccess ||
+      hipStreamSynchronize(c->stream) != hipSuccess)
     return fail(SHK_HIP_STATUS_COPY_FAILED, "device-to-host copy failed");
   return SHK_HIP_STATUS_OK;
 }

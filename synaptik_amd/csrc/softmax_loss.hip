@@ -4,12 +4,16 @@
 //   maximum by Math.max; a +inf maximum maps +inf entries to NaN and the rest to 0 (softmax) or
 //   -inf (log-softmax); a row containing -inf (and no NaN) is evaluated unshifted (shift 0);
 //   addends are (float)exp((double)(x - shift)); the result is (float)exp(shift)/sum or
-//   shift - (float)log(sum). The reference sums addends with Kahan compensation in binary32; the
+//   shift - (float)log(sum). The GPU forms the addends with exp_f32 (fexp.h), which returns
+//   that binary32 value or one of its neighbours (at most 1 ulp away; 0.8% of arguments), and
+//   rows held in registers multiply by a once-rounded reciprocal of the sum.
+//   The reference sums addends with Kahan compensation in binary32; the
 //   GPU sums the same binary32 addends in binary64 through a fixed tree and rounds once, so both
 //   sums are within a few binary32 ulps of the exact sum (reduction-order difference).
 // One 256-thread workgroup owns one row; rows up to 4096 wide are held in registers
 // (one HBM read and one write per element), wider rows are streamed three times.
 #include "common.h"
+#include "fexp.h"
 #include "kernels.h"
 #include <algorithm>
 
@@ -17,9 +21,6 @@ namespace shk {
 namespace {
 
 constexpr int SM_NT = 256;
-#ifndef SHK_SOFTMAX_EXP
-#define SHK_SOFTMAX_EXP(v) ((float)exp((double)(v)))
-#endif
 
 __device__ __forceinline__ int block_or(int v, int* lds) {
   v = wave_or(v);
@@ -39,36 +40,76 @@ struct RowStats {
 };
 
 __device__ __forceinline__ float shifted_exp(float x, float shift) {
-  return SHK_SOFTMAX_EXP(x - shift);
+  return exp_f32(x - shift);
 }
 
 // V float4 per thread in registers (C <= V * 4 * SM_NT, C % 4 == 0).
+//
+// The row statistics use the hardware max / min (v_max_f32 / v_min_f32, which skip NaN and need
+// not order signed zeros) and restore Math.max semantics where they differ, in a branch taken
+// only by rows whose maximum is +inf or a zero: a NaN anywhere makes the maximum NaN, and a zero
+// maximum is +0 when any element is +0. A row holds -inf exactly when its minimum is -inf.
+// A row with a NaN and no +inf already gives NaN everywhere through the sum, as the reference's
+// NaN shift does.
 template <int V>
 __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restrict__ x,
                                                           float* __restrict__ y, float* lse,
                                                           int64_t C, int log_softmax) {
   __shared__ double dl[SM_NT / 64];
-  __shared__ float fl[SM_NT / 64];
-  __shared__ int il[SM_NT / 64];
+  __shared__ float fmx[SM_NT / 64], fmn[SM_NT / 64];
+  __shared__ int il[SM_NT / 64], il2[SM_NT / 64];
   const int64_t r = blockIdx.x;
   const float4* xr = reinterpret_cast<const float4*>(x + r * C);
   float4* yr = reinterpret_cast<float4*>(y + r * C);
   const int C4 = (int)(C / 4);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   float4 v[V];
-  float m = -INFINITY;
-  int neg_inf = 0;
+  float m = -INFINITY, mn = INFINITY;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int c = threadIdx.x + i * SM_NT;
     if (c < C4) {
       v[i] = xr[c];
-      m = java_max(java_max(m, v[i].x), java_max(v[i].y, java_max(v[i].z, v[i].w)));
-      neg_inf |= (v[i].x == -INFINITY) | (v[i].y == -INFINITY) | (v[i].z == -INFINITY) |
-                 (v[i].w == -INFINITY);
+      m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+      mn = fminf(mn, fminf(fminf(v[i].x, v[i].y), fminf(v[i].z, v[i].w)));
     }
   }
-  m = block_max<SM_NT>(m, fl);
-  neg_inf = block_or(neg_inf, il);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    m = fmaxf(m, __shfl_xor(m, o, 64));
+    mn = fminf(mn, __shfl_xor(mn, o, 64));
+  }
+  if (lane == 0) { fmx[w] = m; fmn[w] = mn; }
+  __syncthreads();
+  m = fmx[0];
+  mn = fmn[0];
+#pragma unroll
+  for (int i = 1; i < SM_NT / 64; ++i) {
+    m = fmaxf(m, fmx[i]);
+    mn = fminf(mn, fmn[i]);
+  }
+  if (m == INFINITY || m == 0.0f) {  // block-uniform, rare
+    int nan = 0, pos_zero = 0;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int c = threadIdx.x + i * SM_NT;
+      if (c < C4) {
+        nan |= (v[i].x != v[i].x) | (v[i].y != v[i].y) | (v[i].z != v[i].z) | (v[i].w != v[i].w);
+        pos_zero |= (__float_as_uint(v[i].x) == 0u) | (__float_as_uint(v[i].y) == 0u) |
+                    (__float_as_uint(v[i].z) == 0u) | (__float_as_uint(v[i].w) == 0u);
+      }
+    }
+    nan = wave_or(nan);
+    pos_zero = wave_or(pos_zero);
+    if (lane == 0) { il[w] = nan; il2[w] = pos_zero; }
+    __syncthreads();
+    nan = 0;
+    pos_zero = 0;
+#pragma unroll
+    for (int i = 0; i < SM_NT / 64; ++i) { nan |= il[i]; pos_zero |= il2[i]; }
+    if (nan) m = NAN;
+    else if (m == 0.0f) m = pos_zero ? 0.0f : -0.0f;
+  }
   if (m == INFINITY) {
     const float other = log_softmax ? -INFINITY : 0.0f;
 #pragma unroll
@@ -86,9 +127,10 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restric
     if (lse != nullptr && threadIdx.x == 0) lse[r] = INFINITY;
     return;
   }
+  const bool neg_inf = mn == -INFINITY;
   const float shift = (neg_inf && m == m) ? 0.0f : m;
-  // One binary64 exponential per element: softmax keeps the rounded addends in registers and
-  // divides them by the sum; log-softmax only needs the sum and recomputes x - shift.
+  // One exponential per element: softmax keeps the rounded addends in registers and scales
+  // them by the sum; log-softmax only needs the sum and recomputes x - shift.
   float4 e[V];
   double s = 0.0;
 #pragma unroll
@@ -104,6 +146,11 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restric
   }
   const float sum = (float)block_sum<SM_NT>(s, dl);
   const float logsum = (float)log((double)sum);
+  // Softmax scales by the reciprocal of the sum (one division per row; at most one extra
+  // rounding per element against the reference's quotient). A sum whose reciprocal would leave
+  // the normal range, or a non-finite one, keeps the per-element division.
+  const bool recip = sum >= 0x1p-126f && sum <= 0x1p126f;
+  const float inv = 1.0f / sum;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int c = threadIdx.x + i * SM_NT;
@@ -114,6 +161,11 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restric
         o.y = (v[i].y - shift) - logsum;
         o.z = (v[i].z - shift) - logsum;
         o.w = (v[i].w - shift) - logsum;
+      } else if (recip) {
+        o.x = e[i].x * inv;
+        o.y = e[i].y * inv;
+        o.z = e[i].z * inv;
+        o.w = e[i].w * inv;
       } else {
         o.x = e[i].x / sum;
         o.y = e[i].y / sum;
@@ -123,7 +175,23 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restric
       yr[c] = o;
     }
   }
-  if (lse != nullptr && threadIdx.x == 0) lse[r] = shift + logsum;
+  if (lse != nullptr) {
+    float l = shift + logsum;
+    if (neg_inf && is_finite(m)) {
+      // LOG_SUM_EXP keeps the maximum as its shift even when the row holds -inf
+      // (CpuLogSumExpEmitter.java:4-9); only the softmax values use the unshifted form.
+      double s2 = 0.0;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const int c = threadIdx.x + i * SM_NT;
+        if (c < C4)
+          s2 += ((double)shifted_exp(v[i].x, m) + (double)shifted_exp(v[i].y, m)) +
+                ((double)shifted_exp(v[i].z, m) + (double)shifted_exp(v[i].w, m));
+      }
+      l = m + (float)log((double)(float)block_sum<SM_NT>(s2, dl));
+    }
+    if (threadIdx.x == 0) lse[r] = l;
+  }
 }
 
 // Any width: three streaming passes over the row.
@@ -158,7 +226,15 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_stream(const float* __restr
   const float logsum = (float)log((double)sum);
   for (int64_t c = threadIdx.x; c < C; c += SM_NT)
     yr[c] = log_softmax ? (xr[c] - shift) - logsum : shifted_exp(xr[c], shift) / sum;
-  if (lse != nullptr && threadIdx.x == 0) lse[r] = C == 0 ? -INFINITY : shift + logsum;
+  if (lse != nullptr) {
+    float l = C == 0 ? -INFINITY : shift + logsum;
+    if (neg_inf && is_finite(m)) {  // LOG_SUM_EXP shifts by the maximum (see above)
+      double s2 = 0.0;
+      for (int64_t c = threadIdx.x; c < C; c += SM_NT) s2 += (double)shifted_exp(xr[c], m);
+      l = m + (float)log((double)(float)block_sum<SM_NT>(s2, dl));
+    }
+    if (threadIdx.x == 0) lse[r] = l;
+  }
 }
 
 // dX = y (.) (g - s) [+ k_r * y], s = sum(g (.) y)  (ReductionGradientRules.java:84-90).

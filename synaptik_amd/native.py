@@ -53,6 +53,7 @@ EXPORTED_SYMBOLS = (
     "shk_hip_buffer_upload",
     "shk_hip_buffer_download",
     "shk_hip_buffer_device_pointer",
+    "shk_hip_buffer_download_canonical",
     "shk_hip_program_create",
     "shk_hip_program_release",
     "shk_hip_program_run",
@@ -121,6 +122,10 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
             "shk_hip_buffer_upload": (i32, [vp, u64, vp, u64]),
             "shk_hip_buffer_download": (i32, [vp, u64, vp, u64]),
             "shk_hip_buffer_device_pointer": (i32, [vp, ctypes.POINTER(vp)]),
+            "shk_hip_buffer_download_canonical": (i32, [vp, u32, i32, u32,
+                                                        ctypes.POINTER(ctypes.c_int64),
+                                                        ctypes.POINTER(ctypes.c_int64),
+                                                        ctypes.c_int64, vp, u64, u64]),
             "shk_hip_program_create": (i32, [vp, vp, u64, ctypes.POINTER(vp)]),
             "shk_hip_program_release": (i32, [vp]),
             "shk_hip_program_run": (i32, [vp, u32, ctypes.POINTER(vp), u32, ctypes.POINTER(vp)]),
@@ -230,6 +235,25 @@ class HipBuffer:
         out = np.empty(n, dtype=dt)
         check(self.lib, self.lib.shk_hip_buffer_download(self.handle, offset, out.ctypes.data, out.nbytes))
         return out
+
+    def download_canonical(self, element_width: int, shape, strides=None, storage_offset: int = 0,
+                           boolean: bool = False, maximum_bytes: int | None = None) -> memoryview:
+        """Dense row-major big-endian bytes of a (possibly strided) view of this buffer
+        (`shk_hip_buffer_download_canonical`), as a fresh read-only buffer (the reference hands
+        out a read-only ByteBuffer over its private copy, HostTensorValue.bytes())."""
+        shape = tuple(int(d) for d in shape)
+        rank = len(shape)
+        count = 0 if any(d == 0 for d in shape) else int(np.prod(shape, dtype=np.int64)) if shape else 1
+        nbytes = count * (1 if boolean else int(element_width))
+        if maximum_bytes is None:
+            maximum_bytes = nbytes
+        dims = (ctypes.c_int64 * max(1, rank))(*shape)
+        st = None if strides is None else (ctypes.c_int64 * max(1, rank))(*[int(x) for x in strides])
+        out = np.empty(max(1, nbytes), np.uint8)
+        check(self.lib, self.lib.shk_hip_buffer_download_canonical(
+            self.handle, int(element_width), 1 if boolean else 0, rank, dims, st,
+            int(storage_offset), out.ctypes.data, nbytes, int(maximum_bytes)))
+        return memoryview(out[:nbytes]).toreadonly()
 
     def device_pointer(self) -> int:
         p = ctypes.c_void_p()

@@ -394,3 +394,33 @@ def test_c5_softmax_stress_full_size(ctx):
     np.testing.assert_allclose(L[rows], oracle.logsumexp_rows(x[rows]), rtol=1e-6)
     ref_dx = oracle.softmax_grad_rows(P[rows], dP[rows]) + np.float32(1.0 / R) * P[rows]
     np.testing.assert_allclose(dX[rows], ref_dx, rtol=1e-5, atol=1e-9)
+
+
+@pytest.mark.parametrize("C", [8, 4096, 5000])
+@pytest.mark.parametrize("log", [False, True])
+def test_softmax_special_rows(ctx, C, log):
+    """Rows whose statistics need Math.max semantics (NaN with +inf, zero maxima of either sign,
+    -inf with NaN, a subnormal sum) in the register-resident kernels."""
+    rng = np.random.default_rng(C + 3)
+    x = (rng.standard_normal((10, C)) * 2).astype(np.float32)
+    x[0, 1], x[0, 3] = np.inf, np.nan              # NaN beats +inf: everything NaN
+    x[1, :] = -np.abs(x[1, :]); x[1, 2] = 0.0       # +0 maximum
+    x[2, :] = -np.abs(x[2, :]) - 1; x[2, 5] = -0.0  # -0 maximum
+    x[3, :] = -np.abs(x[3, :]); x[3, 0] = 0.0; x[3, 4] = -0.0
+    x[4, 0], x[4, 6] = -np.inf, np.nan              # -inf with NaN
+    x[5, :] = -np.inf; x[5, 2] = -100.0             # unshifted row with a subnormal sum
+    x[6, :] = np.nan
+    x[7, 1] = np.inf                                # +inf class rule
+    x[8, :] = -np.inf; x[8, 3] = 80.0; x[8, 7] = 85.0  # unshifted, large finite sum
+    got, lse = gpu_softmax(ctx, x, log=log)
+    want = oracle.softmax_rows(x, log=log)
+    want_lse = oracle.logsumexp_rows(x)
+    for g_row, w_row in ((got, want), (lse[:, None], want_lse[:, None])):
+        nan_w = np.isnan(w_row)
+        assert np.array_equal(np.isnan(g_row), nan_w)
+        inf_w = np.isinf(w_row)
+        assert np.array_equal(g_row[inf_w], w_row[inf_w])
+        fin = ~nan_w & ~inf_w
+        np.testing.assert_allclose(g_row[fin], w_row[fin], rtol=2e-6, atol=2e-6 if log else 1e-30)
+        zero = fin & (w_row == 0)
+        assert np.array_equal(np.signbit(g_row[zero]), np.signbit(w_row[zero]))

@@ -148,3 +148,79 @@ def test_fused_bias_gradient_column_sum(ctx, shape):
     np.testing.assert_array_max_ulp(db, oracle.colsum(C), maxulp=1)
     ref = oracle.activation_grad("relu", oracle.matmul(dZ, W), y)
     assert np.linalg.norm(C - ref) / np.linalg.norm(ref) < 1e-5
+
+
+# Shapes that take the large-problem kernel (M, N multiples of 128 with >= 256 output tiles,
+# K a multiple of 32; direct-to-LDS copies, 16x16x4 MFMA): odd and even numbers of k-tiles.
+V2_SHAPES = [(2048, 2048, 96), (2048, 4096, 64), (4096, 2048, 32)]
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("shape", V2_SHAPES)
+def test_large_tile_kernel_integer_bit_exact(ctx, shape, ta, tb):
+    M, N, K = shape
+    rng = np.random.default_rng(M + 3 * N + 7 * K + 2 * ta + tb)
+    A = rng.integers(-3, 4, size=(K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.integers(-3, 4, size=(N, K) if tb else (K, N)).astype(np.float32)
+    C = _gemm_case(ctx, A, B, M, N, K, ta, tb)
+    ref = oracle.matmul(A, B, trans_a=ta, trans_b=tb)
+    assert np.array_equal(C, ref), f"max diff {np.abs(C - ref).max()}"
+
+
+@pytest.mark.parametrize("ta,tb", [(False, True), (False, False), (True, False)])
+def test_large_tile_kernel_gaussian_within_bound(ctx, ta, tb):
+    M, N, K = 2048, 2048, 512
+    rng = np.random.default_rng(17)
+    A = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    C = _gemm_case(ctx, A, B, M, N, K, ta, tb)
+    ref = oracle.matmul(A, B, trans_a=ta, trans_b=tb)
+    Ad = np.abs(A.T if ta else A).astype(np.float64)
+    Bd = np.abs(B.T if tb else B).astype(np.float64)
+    u = 2.0 ** -24
+    bound = 2 * (K * u / (1 - K * u)) * (Ad @ Bd) + 1e-30
+    assert (np.abs(C.astype(np.float64) - ref) <= bound).all()
+    assert np.linalg.norm(C - ref) / np.linalg.norm(ref) < 1e-5
+
+
+@pytest.mark.parametrize("act", ["relu", "tanh", None])
+def test_large_tile_kernel_bias_activation(ctx, act):
+    M, N, K = 2048, 2048, 64
+    rng = np.random.default_rng(23)
+    X = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    W = rng.integers(-3, 4, size=(N, K)).astype(np.float32) * np.float32(0.125)
+    b = rng.standard_normal(N).astype(np.float32)
+    Y = _gemm_case(ctx, X, W, M, N, K, False, True, bias=b, act=act)
+    assert np.array_equal(Y, oracle.linear_forward(X, W, b, act))
+
+
+@pytest.mark.parametrize("act", ["relu", "sigmoid"])
+def test_large_tile_kernel_activation_gradient_and_column_sum(ctx, act):
+    M, N, K = 2048, 2048, 64
+    rng = np.random.default_rng(29)
+    dZ = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    W = rng.integers(-3, 4, size=(K, N)).astype(np.float32)
+    y = oracle.activation(act, rng.standard_normal((M, N)).astype(np.float32))
+    pb = ProgramBuilder()
+    sa, sb, sy = pb.input(M * K), pb.input(K * N), pb.input(M * N)
+    sc, sd = pb.output(M * N), pb.output(N)
+    pb.gemm(sa, sb, sc, M, N, K, aux=sy, act=act, act_grad=True, colsum=sd)
+    C, db = run_program(ctx, pb, [dZ, W, y], [sc, sd])
+    C = C.reshape(M, N)
+    assert np.array_equal(C, oracle.activation_grad(act, oracle.matmul(dZ, W), y))
+    np.testing.assert_array_max_ulp(db, oracle.colsum(C), maxulp=1)
+
+
+def test_large_tile_kernel_accumulate(ctx):
+    M, N, K = 2048, 2048, 32
+    rng = np.random.default_rng(31)
+    A = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    B = rng.integers(-3, 4, size=(N, K)).astype(np.float32)
+    C0 = rng.integers(-8, 9, size=(M, N)).astype(np.float32)
+    pb = ProgramBuilder()
+    sa, sb, sc = pb.input(M * K), pb.input(N * K), pb.output(M * N)
+    pb.copy(pb.input(M * N), sc, M * N)
+    pb.gemm(sa, sb, sc, M, N, K, trans_b=True, accumulate=True)
+    (C,) = run_program(ctx, pb, [A, B, C0], [sc])
+    assert np.array_equal(C.reshape(M, N), C0 + oracle.matmul(A, B, trans_b=True))

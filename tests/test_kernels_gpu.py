@@ -355,16 +355,26 @@ def test_c2_fused_layer_forward_backward_full_size(ctx):
     dY = rng.standard_normal((B, O)).astype(np.float32)
     pb, outs = lower_dense_layer(B, I, O, "relu", "in_out")
     Y, dX, dW, db = run_program(ctx, pb, [X, W, b, dY], list(outs))
+    Y = Y.reshape(B, O)
     Yr = oracle.activation("relu", oracle.matmul(X, W))
-    dZ = oracle.activation_grad("relu", dY, Yr)
+    # the backward pass differentiates through the forward values it computed, as the reference
+    # does: the oracle's backward starts from the GPU's Y, so an activation within rounding of 0
+    # (whose mask may differ between two reduction orders) does not change the comparison
+    dZ = oracle.activation_grad("relu", dY, Y)
     dXr = oracle.matmul(dZ, W, trans_b=True)
     dWr = oracle.matmul(X, dZ, trans_a=True)
     dbr = oracle.colsum(dZ)
     for got, want in [(Y, Yr), (dX, dXr), (dW, dWr), (db, dbr)]:
         rel = np.linalg.norm(got.reshape(want.shape) - want) / np.linalg.norm(want)
         assert rel <= 1e-5, rel
-    # the ReLU mask (an index/predicate result) is bit-exact
-    assert np.array_equal(Y.reshape(B, O) > 0, Yr > 0)
+    # the ReLU mask (a predicate result) is exact wherever the pre-activation is farther from 0
+    # than the GEMM's error bound 2 gamma_K sum|x||w|
+    u = 2.0 ** -24
+    bound = 2 * (I * u / (1 - I * u)) * (np.abs(X).astype(np.float64) @ np.abs(W).astype(np.float64))
+    pre = oracle.matmul(X, W)
+    decided = np.abs(pre) > bound
+    assert decided.mean() > 0.99
+    assert np.array_equal((Y > 0)[decided], (Yr > 0)[decided])
 
 
 def test_c5_softmax_stress_full_size(ctx):

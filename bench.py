@@ -42,7 +42,7 @@ def gemm_flops() -> float:
 
 def measured_gemm_traffic():
     """HBM bytes per 4096^3 GEMM launch from the committed rocprofv3 --pmc summary, or None."""
-    f = ROOT / "profiles" / "gemm_f32_mfma_4096_traffic.md"
+    f = ROOT / "profiles" / "gemm_f32_v2_4096_traffic.md"
     try:
         for line in f.read_text().splitlines():
             if line.startswith("traffic_bytes_per_launch:"):
@@ -389,7 +389,7 @@ def main() -> int:
                    "layers": "4096->4096x4 hidden->4096 ReLU", "global_batch": BATCH,
                    "loss": "MSE mean", "optimizer": f"SGD lr={LR} momentum={MOMENTUM}",
                    "parallelism": "single GPU", "objective_after": loss},
-        "roofline": {"bound": "mfma", "kernel": "gemm_f32_mfma (14 per step, 4096^3 each)",
+        "roofline": {"bound": "mfma", "kernel": "gemm_f32_v2 (14 per step, 4096^3 each)",
                      "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
                      "traffic": measured_gemm_traffic()},

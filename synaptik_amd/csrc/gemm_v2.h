@@ -67,7 +67,8 @@ struct V2Loader {
     }
   }
   // Copy I of this wave for the k-tile whose element (row 0, k 0) is `tile`, into stage `lds`:
-  // global_load_lds_dwordx4 with the tile origin in SGPRs and a per-lane 32-bit offset.
+  // global_load_lds_dwordx4 with the tile origin in SGPRs, a per-lane 32-bit offset and the LDS
+  // destination in M0.
   // Written as inline assembly so that the compiler does not track the copies (it would make
   // every LDS read wait for all copies in flight, including those into the other stage); the
   // kernel waits for them itself (v2_wait_all) before each barrier.
@@ -75,10 +76,10 @@ struct V2Loader {
   __device__ __forceinline__ void issue(const float* tile, float* lds) const {
     const uint32_t dst =
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)lds + I * 4096u + wdst;
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+    asm volatile("global_load_lds_dwordx4 %0, %1"
                  :
-                 : "v"(voff[I]), "s"(tile), "s"(dst)
-                 : "memory", "m0");
+                 : "v"(voff[I]), "s"(tile), "{m0}"(dst)
+                 : "memory");
   }
 };
 

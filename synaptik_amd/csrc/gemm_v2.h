@@ -23,6 +23,7 @@
 // reassociate anyway (the reference contract allows it, foundational-modules.md:423-425).
 #pragma once
 #include "gemm_tile.h"
+#include "gemm_v2_layout.h"
 
 namespace shk {
 namespace {
@@ -31,18 +32,6 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int V2_BM = 128, V2_BN = 128, V2_BK = 32, V2_NT = 256;
 constexpr int V2_TILE = 128 * 32;  // floats per operand per stage
-
-// LDS float offset of chunk c (k = 4c..4c+3) of row r in a K-contiguous tile: rows 2L and 2L+1
-// share one 256-byte line whose 16 chunk slots are permuted by XOR with L mod 16.
-__host__ __device__ constexpr int v2_kmaj_off(int r, int c) {
-  return ((r >> 1) * 16 + ((((r & 1) << 3) | c) ^ ((r >> 1) & 15))) * 4;
-}
-// LDS float offset of element (k, m) in an M/N-contiguous tile: 32 chunks of four per k-row,
-// chunk slot XORed with 4 * ((k / 4) mod 4), so the four lane groups of a fragment read (rows
-// k = 16h + 4g + s) land on four different 16-bank groups.
-__host__ __device__ constexpr int v2_mnmaj_off(int k, int m) {
-  return k * 128 + (((m >> 2) ^ (((k >> 2) & 3) << 2)) << 2) + (m & 3);
-}
 
 // Per-lane source offsets (bytes, relative to the tile origin) of the four 16-byte copies this
 // thread issues per operand per k-tile, and where they land.
@@ -57,11 +46,10 @@ struct V2Loader {
     for (int i = 0; i < 4; ++i) {
       const int q = (i * 4 + w) * 64 + lane;  // destination chunk of this lane
       if constexpr (KMAJ) {
-        const int L = q >> 4, t = (q & 15) ^ (L & 15);
-        const int r = 2 * L + (t >> 3), c = t & 7;
+        const int src = v2_kmaj_src(q), r = src >> 3, c = src & 7;
         voff[i] = (uint32_t)((r * ld + 4 * c) * 4);
       } else {
-        const int k = q >> 5, c = (q & 31) ^ (((k >> 2) & 3) << 2);
+        const int src = v2_mnmaj_src(q), k = src >> 5, c = src & 31;
         voff[i] = (uint32_t)((k * ld + 4 * c) * 4);
       }
     }

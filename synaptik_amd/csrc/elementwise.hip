@@ -204,15 +204,31 @@ __global__ void __launch_bounds__(256) colsum_pass1(const float* __restrict__ x,
   if (w == 0 && col < N)
     part[(int64_t)blockIdx.y * N + col] = ((lds[0][lane] + lds[1][lane]) + lds[2][lane]) + lds[3][lane];
 }
-__global__ void colsum_pass2(const double* part, float* out, int64_t P, int64_t N,
-                             double divisor, int accumulate) {
-  const int64_t col = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (col >= N) return;
-  double s = 0.0;
-  for (int64_t i = 0; i < P; ++i) s += part[i * N + col];
-  float v = (float)(s / divisor);
-  if (accumulate) v = out[col] + v;
-  out[col] = v;
+// Column sums, pass 2: block x finishes 64 columns; wave w adds partial rows w, w + 4, ... in
+// two interleaved chains (independent loads in flight), then the chains and the four waves are
+// combined in a fixed order, so results are run-to-run identical.
+__global__ void __launch_bounds__(256) colsum_pass2(const double* part, float* out, int64_t P,
+                                                    int64_t N, double divisor, int accumulate) {
+  __shared__ double lds[4][CS_COLS];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t col = (int64_t)blockIdx.x * CS_COLS + lane;
+  double s0 = 0.0, s1 = 0.0;
+  if (col < N) {
+    int64_t i = w;
+    for (; i + 4 < P; i += 8) {
+      s0 += part[i * N + col];
+      s1 += part[(i + 4) * N + col];
+    }
+    if (i < P) s0 += part[i * N + col];
+  }
+  lds[w][lane] = s0 + s1;
+  __syncthreads();
+  if (w == 0 && col < N) {
+    const double s = ((lds[0][lane] + lds[1][lane]) + lds[2][lane]) + lds[3][lane];
+    float v = (float)(s / divisor);
+    if (accumulate) v = out[col] + v;
+    out[col] = v;
+  }
 }
 
 // Row reductions: one workgroup per row, binary64 accumulation for SUM/MEAN/LSE.
@@ -357,16 +373,16 @@ hipError_t launch_colsum(const float* x, float* out, int64_t R, int64_t N, int64
     dim3 g1((unsigned)((N + CS_COLS - 1) / CS_COLS), (unsigned)P);
     hipLaunchKernelGGL(colsum_pass1, g1, dim3(256), 0, s, x, partial, R, N, ldx, rows);
   }
-  hipLaunchKernelGGL(colsum_pass2, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s, partial,
-                     out, P, N, divisor, accumulate);
+  hipLaunchKernelGGL(colsum_pass2, dim3((unsigned)((N + CS_COLS - 1) / CS_COLS)), dim3(256), 0, s,
+                     partial, out, P, N, divisor, accumulate);
   return hipGetLastError();
 }
 
 hipError_t launch_colsum_finish(const double* partial, float* out, int64_t P, int64_t N,
                                 hipStream_t s) {
   if (N <= 0) return hipSuccess;
-  hipLaunchKernelGGL(colsum_pass2, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s, partial,
-                     out, P, N, 1.0, 0);
+  hipLaunchKernelGGL(colsum_pass2, dim3((unsigned)((N + CS_COLS - 1) / CS_COLS)), dim3(256), 0, s,
+                     partial, out, P, N, 1.0, 0);
   return hipGetLastError();
 }
 

@@ -124,7 +124,7 @@ int64_t splitk_slices(int64_t M, int64_t N, int64_t K) {
 }
 int64_t splitk_chunk(int64_t K, int64_t s) {
   const int64_t c = (K + s - 1) / s;
-  return ((c + 15) / 16) * 16;  // whole BK tiles per slice
+  return ((c + 31) / 32) * 32;  // whole k-tiles of either tile kernel (BK 16 or 32) per slice
 }
 }  // namespace
 

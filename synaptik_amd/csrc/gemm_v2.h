@@ -126,8 +126,11 @@ gemm_f32_v2(GemmParams p) {
   const int l16 = lane & 15, g = lane >> 4;
 
   // operand tile origins at k = 0, and the per-k-tile advance
-  const float* a_tile = KA ? p.A + m0 * p.lda : p.A + m0;
-  const float* b_tile = KB ? p.B + n0 * p.ldb : p.B + n0;
+  // split-K: block row y covers k in [y * kchunk, min(K, (y + 1) * kchunk))
+  const int64_t k_begin = p.kchunk > 0 ? (int64_t)blockIdx.y * p.kchunk : 0;
+  const int64_t k_len = p.kchunk > 0 ? std::min<int64_t>(p.kchunk, p.K - k_begin) : p.K;
+  const float* a_tile = KA ? p.A + m0 * p.lda + k_begin : p.A + m0 + k_begin * p.lda;
+  const float* b_tile = KB ? p.B + n0 * p.ldb + k_begin : p.B + n0 + k_begin * p.ldb;
   const int64_t a_step = KA ? V2_BK : V2_BK * p.lda;
   const int64_t b_step = KB ? V2_BK : V2_BK * p.ldb;
   V2Loader<KA> la;
@@ -155,7 +158,7 @@ gemm_f32_v2(GemmParams p) {
     });
   });
 
-  const int nk = (int)(p.K / V2_BK);
+  const int nk = (int)(k_len / V2_BK);
   // 64 MFMAs of one half-tile in 8 groups of 8 (group q: MFMA s = q / 2 of blocks
   // i = 2 (q % 2) .. +1, j = 0..3); after each group, side(q) issues that group's share of the
   // LDS reads and copies. The scheduling barriers keep this order: reads and copies spread over
@@ -256,6 +259,18 @@ gemm_f32_v2(GemmParams p) {
   // Epilogue. Accumulator r of block (i, j) holds row 16i + 4g + r, column 16j + l16 of the
   // wave's 64x64 sub-tile.
   const int64_t row_w = m0 + wm * 64 + 4 * g, col_w = n0 + wn * 64 + l16;
+  if (p.partial != nullptr) {
+    // split-K: raw partial sums, reduced (and given the epilogue) by gemm_splitk_reduce
+    float* part = p.partial + (int64_t)blockIdx.y * p.M * p.N;
+    static_for<4>([&](auto i) {
+      static_for<4>([&](auto j) {
+        constexpr int I = decltype(i)::value, J = decltype(j)::value;
+        float* dst = part + (row_w + 16 * I) * p.N + col_w + 16 * J;
+        static_for<4>([&](auto r) { dst[decltype(r)::value * p.N] = acc[I][J][decltype(r)::value]; });
+      });
+    });
+    return;
+  }
   if (p.upd.pn != nullptr) {
     const GemmUpdate& u = p.upd;
     const UpdateCtx uc = update_ctx(u);
@@ -316,11 +331,16 @@ gemm_f32_v2(GemmParams p) {
   });
 }
 
-// Whether the large-problem kernel handles this GEMM (see the header comment).
+// Whether the large-problem kernel handles this GEMM (see the header comment): whole tiles,
+// whole 32-deep k-tiles (per split-K slice when p.kchunk > 0), 16-byte operand loads, and
+// enough workgroups to fill the chip (output tiles times slices).
 inline bool v2_eligible(const GemmParams& p, bool va, bool vb) {
-  return va && vb && p.kchunk == 0 && p.partial == nullptr && p.M % V2_BM == 0 &&
-         p.N % V2_BN == 0 && p.K % V2_BK == 0 && p.K >= V2_BK &&
-         (p.M / V2_BM) * (p.N / V2_BN) >= 256 && (p.M / V2_BM) * (p.N / V2_BN) < (1LL << 31) &&
+  if (!va || !vb || p.M % V2_BM != 0 || p.N % V2_BN != 0 || p.K % V2_BK != 0 || p.K < V2_BK)
+    return false;
+  if (p.kchunk > 0 && (p.kchunk % V2_BK != 0 || p.partial == nullptr)) return false;
+  const int64_t tiles = (p.M / V2_BM) * (p.N / V2_BN);
+  const int64_t slices = p.kchunk > 0 ? (p.K + p.kchunk - 1) / p.kchunk : 1;
+  return tiles * slices >= 256 && tiles < (1LL << 31) && slices < 65536 &&
          p.M * std::max(p.lda, p.ldb) < (1LL << 31) && p.K * std::max(p.lda, p.ldb) < (1LL << 31);
 }
 
@@ -328,7 +348,8 @@ template <bool TA, bool TB>
 hipError_t launch_v2(const GemmParams& p, hipStream_t s) {
   g_colsum_rows = (p.M / V2_BM) * 2;
   const unsigned tiles = (unsigned)((p.M / V2_BM) * (p.N / V2_BN));
-  hipLaunchKernelGGL((gemm_f32_v2<!TA, TB>), dim3(tiles), dim3(V2_NT), 0, s, p);
+  const unsigned slices = p.kchunk > 0 ? (unsigned)((p.K + p.kchunk - 1) / p.kchunk) : 1u;
+  hipLaunchKernelGGL((gemm_f32_v2<!TA, TB>), dim3(tiles, slices), dim3(V2_NT), 0, s, p);
   return hipGetLastError();
 }
 

@@ -224,3 +224,17 @@ def test_large_tile_kernel_accumulate(ctx):
     pb.gemm(sa, sb, sc, M, N, K, trans_b=True, accumulate=True)
     (C,) = run_program(ctx, pb, [A, B, C0], [sc])
     assert np.array_equal(C.reshape(M, N), C0 + oracle.matmul(A, B, trans_b=True))
+
+
+@pytest.mark.parametrize("ta,tb", [(True, False), (False, True), (False, False)])
+def test_large_tile_kernel_split_k(ctx, ta, tb):
+    """Few output tiles and a long K: split-K slices on the large-problem kernel, reduced in slice
+    order; integer operands keep it bit-exact, bias and ReLU applied after the reduction."""
+    M, N, K = 1024, 1024, 4096
+    rng = np.random.default_rng(37 + ta + 2 * tb)
+    A = rng.integers(-3, 4, size=(K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.integers(-3, 4, size=(N, K) if tb else (K, N)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    C = _gemm_case(ctx, A, B, M, N, K, ta, tb, bias=b, act="relu")
+    Z = oracle.matmul(A, B, trans_a=ta, trans_b=tb)
+    assert np.array_equal(C, oracle.activation("relu", Z + b))

@@ -257,7 +257,11 @@ gemm_f32_v2(GemmParams p) {
   if (kt < nk) step(std::integral_constant<int, 0>{}, kt);
 
   // Epilogue. Accumulator r of block (i, j) holds row 16i + 4g + r, column 16j + l16 of the
-  // wave's 64x64 sub-tile.
+  // wave's 64x64 sub-tile. Split-K partials are written from that layout directly; otherwise
+  // the sub-tile is transposed through this wave's own 16 KB of LDS (row-major, 16-byte chunks
+  // XOR-swizzled by row) so that every global access of the epilogue is a 16-byte row segment:
+  // lane (q = lane % 16, rg = lane / 16) then owns columns 4q..4q+3 of rows rg + 4t, t < 16,
+  // and each store instruction writes four full 256-byte row segments.
   const int64_t row_w = m0 + wm * 64 + 4 * g, col_w = n0 + wn * 64 + l16;
   if (p.partial != nullptr) {
     // split-K: raw partial sums, reduced (and given the epilogue) by gemm_splitk_reduce
@@ -271,64 +275,89 @@ gemm_f32_v2(GemmParams p) {
     });
     return;
   }
+  v2_wait_all();
+  v2_barrier();  // every wave has finished reading its fragments: the stages are free
+  float* stage = wave == 0 ? As0 : wave == 1 ? Bs0 : wave == 2 ? As1 : Bs1;
+  static_for<4>([&](auto i) {
+    static_for<4>([&](auto j) {
+      constexpr int I = decltype(i)::value, J = decltype(j)::value;
+      static_for<4>([&](auto r) {
+        constexpr int R = decltype(r)::value;
+        const int row = 16 * I + 4 * g + R, col = 16 * J + l16;
+        stage[row * 64 + (((col >> 2) ^ (row & 15)) << 2) + (col & 3)] = acc[I][J][R];
+      });
+    });
+  });
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are complete
+  const int q = lane & 15, rg = lane >> 4;
+  auto tile_row = [&](int t) -> floatx4 {
+    const int row = rg + 4 * t;
+    return *reinterpret_cast<const floatx4*>(stage + row * 64 + ((q ^ (row & 15)) << 2));
+  };
+  const int64_t row_e = m0 + wm * 64 + rg, col_e = n0 + wn * 64 + 4 * q;
   if (p.upd.pn != nullptr) {
     const GemmUpdate& u = p.upd;
     const UpdateCtx uc = update_ctx(u);
     bool ok = uc.k.ok;
-    static_for<4>([&](auto i) {
-      static_for<4>([&](auto j) {
-        constexpr int I = decltype(i)::value, J = decltype(j)::value;
-        const int64_t e0 = (row_w + 16 * I) * p.N + col_w + 16 * J;
-        float pv[4], mv[4], vv[4];
-        static_for<4>([&](auto r) {
-          constexpr int R = decltype(r)::value;
-          pv[R] = u.p[e0 + R * p.N];
-          mv[R] = u.m != nullptr ? u.m[e0 + R * p.N] : 0.0f;
-          vv[R] = u.kind != 0 ? u.v[e0 + R * p.N] : 0.0f;
-        });
-        static_for<4>([&](auto r) {
-          constexpr int R = decltype(r)::value;
-          ok &= update_element(u, uc, pv[R], acc[I][J][R], mv[R], vv[R], e0 + R * p.N);
-        });
-        __builtin_amdgcn_sched_barrier(0);
+    for (int t = 0; t < 16; ++t) {
+      const int64_t e = (row_e + 4 * t) * p.N + col_e;
+      const floatx4 gv = tile_row(t);
+      const floatx4 pv = *reinterpret_cast<const floatx4*>(u.p + e);
+      const floatx4 mv = u.m != nullptr ? *reinterpret_cast<const floatx4*>(u.m + e) : floatx4{0.f, 0.f, 0.f, 0.f};
+      const floatx4 vv = u.kind != 0 ? *reinterpret_cast<const floatx4*>(u.v + e) : floatx4{0.f, 0.f, 0.f, 0.f};
+      floatx4 pc, mc, vc = floatx4{0.f, 0.f, 0.f, 0.f};
+      static_for<4>([&](auto c) {
+        constexpr int C = decltype(c)::value;
+        float pe, me, ve = 0.0f;
+        if (u.kind == 0) ok &= sgd_element(u, uc.first, pv[C], gv[C], mv[C], pe, me);
+        else ok &= adam_element(u, uc.k, pv[C], gv[C], mv[C], vv[C], pe, me, ve);
+        pc[C] = pe;
+        mc[C] = me;
+        vc[C] = ve;
       });
-    });
+      *reinterpret_cast<floatx4*>(u.pn + e) = pc;
+      if (u.mn != nullptr) *reinterpret_cast<floatx4*>(u.mn + e) = mc;
+      if (u.kind != 0) *reinterpret_cast<floatx4*>(u.vn + e) = vc;
+    }
     update_flag(u, uc, ok);
     return;
   }
-  static_for<4>([&](auto j) {
-    constexpr int J = decltype(j)::value;
-    const int64_t col = col_w + 16 * J;
-    const float bias = p.bias != nullptr ? p.bias[col] : 0.f;
-    double csum = 0.0;
-    static_for<4>([&](auto i) {
-      constexpr int I = decltype(i)::value;
-      const int64_t row0 = row_w + 16 * I;
-      float* cptr = p.C + row0 * p.ldc + col;
-      const float* aptr = p.mode == 1 ? p.aux + row0 * p.ldaux + col : nullptr;
-      static_for<4>([&](auto r) {
-        constexpr int R = decltype(r)::value;
-        float v = acc[I][J][R];
-        if (p.mode == 0) {
-          if (p.bias != nullptr) v = v + bias;
-          v = apply_act(p.act, v);
-        } else {
-          v = act_grad(p.act, v, aptr[R * p.ldaux]);
-        }
-        float* dst = cptr + R * p.ldc;
-        if (p.accumulate) v = *dst + v;
-        *dst = v;
-        csum += (double)v;
+  floatx4 bias = floatx4{0.f, 0.f, 0.f, 0.f};
+  if (p.bias != nullptr) bias = *reinterpret_cast<const floatx4*>(p.bias + col_e);
+  double cs[4] = {0.0, 0.0, 0.0, 0.0};  // fused column sums of this lane's stored values
+  for (int t = 0; t < 16; ++t) {
+    const int64_t row = row_e + 4 * t;
+    floatx4 v = tile_row(t);
+    if (p.mode == 0) {
+      if (p.bias != nullptr) v = floatx4{v[0] + bias[0], v[1] + bias[1], v[2] + bias[2], v[3] + bias[3]};
+      static_for<4>([&](auto c) { v[decltype(c)::value] = apply_act(p.act, v[decltype(c)::value]); });
+    } else {
+      const floatx4 y = *reinterpret_cast<const floatx4*>(p.aux + row * p.ldaux + col_e);
+      static_for<4>([&](auto c) {
+        constexpr int C = decltype(c)::value;
+        v[C] = act_grad(p.act, v[C], y[C]);
       });
-      __builtin_amdgcn_sched_barrier(0);
-    });
-    if (p.colsum_partial != nullptr) {
-      // lanes l16 + 16g hold the same column: one partial row per wave
-      csum += __shfl_xor(csum, 16, 64);
-      csum += __shfl_xor(csum, 32, 64);
-      if (g == 0) p.colsum_partial[((int64_t)tm * 2 + wm) * p.N + col] = csum;
     }
-  });
+    floatx4* dst = reinterpret_cast<floatx4*>(p.C + row * p.ldc + col_e);
+    if (p.accumulate) {
+      const floatx4 o = *dst;
+      v = floatx4{o[0] + v[0], o[1] + v[1], o[2] + v[2], o[3] + v[3]};
+    }
+    *dst = v;
+    static_for<4>([&](auto c) { cs[decltype(c)::value] += (double)v[decltype(c)::value]; });
+  }
+  if (p.colsum_partial != nullptr) {
+    // lanes q + 16 rg hold the same columns: one partial row per wave
+    static_for<4>([&](auto c) {
+      constexpr int C = decltype(c)::value;
+      cs[C] += __shfl_xor(cs[C], 16, 64);
+      cs[C] += __shfl_xor(cs[C], 32, 64);
+    });
+    if (rg == 0) {
+      double* dst = p.colsum_partial + ((int64_t)tm * 2 + wm) * p.N + col_e;
+      static_for<4>([&](auto c) { dst[decltype(c)::value] = cs[decltype(c)::value]; });
+    }
+  }
 }
 
 // Whether the large-problem kernel handles this GEMM (see the header comment): whole tiles,
@@ -338,6 +367,19 @@ inline bool v2_eligible(const GemmParams& p, bool va, bool vb) {
   if (!va || !vb || p.M % V2_BM != 0 || p.N % V2_BN != 0 || p.K % V2_BK != 0 || p.K < V2_BK)
     return false;
   if (p.kchunk > 0 && (p.kchunk % V2_BK != 0 || p.partial == nullptr)) return false;
+  // the transposed epilogue moves 16-byte row segments
+  auto al = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; };
+  if (p.kchunk == 0) {
+    if (p.upd.pn != nullptr) {
+      const GemmUpdate& u = p.upd;
+      if (!al(u.p) || !al(u.pn) || (u.m != nullptr && (!al(u.m) || !al(u.mn))) ||
+          (u.kind != 0 && (!al(u.v) || !al(u.vn))))
+        return false;
+    } else {
+      if (!al(p.C) || p.ldc % 4 != 0 || (p.bias != nullptr && !al(p.bias))) return false;
+      if (p.mode == 1 && (!al(p.aux) || p.ldaux % 4 != 0)) return false;
+    }
+  }
   const int64_t tiles = (p.M / V2_BM) * (p.N / V2_BN);
   const int64_t slices = p.kchunk > 0 ? (p.K + p.kchunk - 1) / p.kchunk : 1;
   return tiles * slices >= 256 && tiles < (1LL << 31) && slices < 65536 &&

@@ -238,3 +238,26 @@ def test_large_tile_kernel_split_k(ctx, ta, tb):
     C = _gemm_case(ctx, A, B, M, N, K, ta, tb, bias=b, act="relu")
     Z = oracle.matmul(A, B, trans_a=ta, trans_b=tb)
     assert np.array_equal(C, oracle.activation("relu", Z + b))
+
+
+def test_large_tile_kernel_strided_operands_and_output(ctx):
+    """Leading dimensions wider than the logical extents (a column block of wider storage for A,
+    B and C, and of the aux operand): the large-problem kernel reads and writes only the block."""
+    M, N, K = 2048, 2048, 64
+    lda, ldb, ldc = K + 32, N + 128, N + 64
+    rng = np.random.default_rng(41)
+    A = rng.integers(-3, 4, size=(M, lda)).astype(np.float32)
+    B = rng.integers(-3, 4, size=(K, ldb)).astype(np.float32)
+    y = oracle.activation("relu", rng.standard_normal((M, ldc)).astype(np.float32))
+    C0 = np.full((M, ldc), 7.0, np.float32)
+    pb = ProgramBuilder()
+    sa, sb, sy = pb.input(A.size), pb.input(B.size), pb.input(y.size)
+    sc = pb.output(C0.size)
+    pb.copy(pb.input(C0.size), sc, C0.size)
+    pb.gemm(sa, sb, sc, M, N, K, lda=lda, ldb=ldb, ldc=ldc, aux=sy, ldaux=ldc, act="relu",
+            act_grad=True)
+    (C,) = run_program(ctx, pb, [A, B, y, C0], [sc])
+    C = C.reshape(M, ldc)
+    Z = oracle.matmul(np.ascontiguousarray(A[:, :K]), np.ascontiguousarray(B[:, :N]))
+    assert np.array_equal(C[:, :N], oracle.activation_grad("relu", Z, np.ascontiguousarray(y[:, :N])))
+    assert (C[:, N:] == 7.0).all()

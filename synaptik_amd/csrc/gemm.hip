@@ -100,6 +100,68 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(GemmParams p, int spli
   if (upd) update_flag(p.upd, uc, ok);
 }
 
+// The same reduction four consecutive outputs at a time (N, ldc, ldaux multiples of 4 and every
+// pointer 16-byte aligned): float4 loads of the slices and float4 epilogue traffic.
+__global__ void __launch_bounds__(256) gemm_splitk_reduce4(GemmParams p, int splits) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const int64_t groups = p.M * p.N / 4;
+  const int64_t plane = p.M * p.N;
+  const bool upd = p.upd.pn != nullptr;
+  UpdateCtx uc{};
+  bool ok = true;
+  if (upd) {
+    uc = update_ctx(p.upd);
+    ok = uc.k.ok;
+  }
+  for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < groups; q += (int64_t)gridDim.x * 256) {
+    const int64_t e = 4 * q, row = e / p.N, col = e - row * p.N;
+    f4 v = *reinterpret_cast<const f4*>(p.partial + e);
+    for (int sidx = 1; sidx < splits; ++sidx) {
+      const f4 w = *reinterpret_cast<const f4*>(p.partial + sidx * plane + e);
+      v = f4{v[0] + w[0], v[1] + w[1], v[2] + w[2], v[3] + w[3]};
+    }
+    if (upd) {
+      const GemmUpdate& u = p.upd;
+      const f4 pv = *reinterpret_cast<const f4*>(u.p + e);
+      const f4 mv = u.m != nullptr ? *reinterpret_cast<const f4*>(u.m + e) : f4{0.f, 0.f, 0.f, 0.f};
+      const f4 vv = u.kind != 0 ? *reinterpret_cast<const f4*>(u.v + e) : f4{0.f, 0.f, 0.f, 0.f};
+      f4 pc, mc, vc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float pe, me, ve = 0.0f;
+        if (u.kind == 0) ok &= sgd_element(u, uc.first, pv[c], v[c], mv[c], pe, me);
+        else ok &= adam_element(u, uc.k, pv[c], v[c], mv[c], vv[c], pe, me, ve);
+        pc[c] = pe;
+        mc[c] = me;
+        vc[c] = ve;
+      }
+      *reinterpret_cast<f4*>(u.pn + e) = pc;
+      if (u.mn != nullptr) *reinterpret_cast<f4*>(u.mn + e) = mc;
+      if (u.kind != 0) *reinterpret_cast<f4*>(u.vn + e) = vc;
+      continue;
+    }
+    if (p.mode == 0) {
+      if (p.bias != nullptr) {
+        const f4 b = *reinterpret_cast<const f4*>(p.bias + col);
+        v = f4{v[0] + b[0], v[1] + b[1], v[2] + b[2], v[3] + b[3]};
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[c] = apply_act(p.act, v[c]);
+    } else {
+      const f4 y = *reinterpret_cast<const f4*>(p.aux + row * p.ldaux + col);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[c] = act_grad(p.act, v[c], y[c]);
+    }
+    f4* dst = reinterpret_cast<f4*>(p.C + row * p.ldc + col);
+    if (p.accumulate) {
+      const f4 o = *dst;
+      v = f4{o[0] + v[0], o[1] + v[1], o[2] + v[2], o[3] + v[3]};
+    }
+    *dst = v;
+  }
+  if (upd) update_flag(p.upd, uc, ok);
+}
+
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
 hipError_t launch_tiles(const GemmParams& p, bool va, bool vb, bool split, hipStream_t s) {
@@ -181,8 +243,22 @@ hipError_t launch_gemm_core(const GemmParams& in, float* workspace, hipStream_t 
     hipError_t e = launch_tiles(p, va, vb, true, s);
     if (e != hipSuccess) return e;
     const int64_t total = p.M * p.N;
-    const unsigned blocks = (unsigned)std::min<int64_t>(65536, (total + 255) / 256);
-    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(blocks), dim3(256), 0, s, p, slices);
+    bool vec = p.N % 4 == 0 && aligned16(p.partial);
+    if (p.upd.pn != nullptr) {
+      const GemmUpdate& u = p.upd;
+      vec = vec && aligned16(u.p) && aligned16(u.pn) && (u.m == nullptr || (aligned16(u.m) && aligned16(u.mn))) &&
+            (u.kind == 0 || (aligned16(u.v) && aligned16(u.vn)));
+    } else {
+      vec = vec && aligned16(p.C) && p.ldc % 4 == 0 && (p.bias == nullptr || aligned16(p.bias)) &&
+            (p.mode != 1 || (aligned16(p.aux) && p.ldaux % 4 == 0));
+    }
+    if (vec) {
+      const unsigned blocks = (unsigned)std::min<int64_t>(65536, (total / 4 + 255) / 256);
+      hipLaunchKernelGGL(gemm_splitk_reduce4, dim3(blocks), dim3(256), 0, s, p, slices);
+    } else {
+      const unsigned blocks = (unsigned)std::min<int64_t>(65536, (total + 255) / 256);
+      hipLaunchKernelGGL(gemm_splitk_reduce, dim3(blocks), dim3(256), 0, s, p, slices);
+    }
     return hipGetLastError();
   }
   if (p.K == 1) {

@@ -233,8 +233,9 @@ def test_mse_against_oracle(ctx, n, reduction):
 
 @pytest.mark.parametrize("dtype", ["i64", "i32"])
 @pytest.mark.parametrize("ignore", [None, -100])
-def test_index_cross_entropy_against_oracle(ctx, dtype, ignore):
-    R, C = 1024, 10
+@pytest.mark.parametrize("shape", [(1024, 10), (9000, 10), (300, 100)], ids=["one-workgroup", "many-rows", "many-classes"])
+def test_index_cross_entropy_against_oracle(ctx, dtype, ignore, shape):
+    R, C = shape
     rng = np.random.default_rng(9)
     logits = (rng.standard_normal((R, C)) * 3).astype(np.float32)
     y = rng.integers(0, C, R)
@@ -252,8 +253,9 @@ def test_index_cross_entropy_against_oracle(ctx, dtype, ignore):
                                rtol=1e-5, atol=1e-9)
 
 
-def test_index_cross_entropy_out_of_bounds_status(ctx):
-    R, C = 16, 4
+@pytest.mark.parametrize("shape", [(16, 4), (9000, 4)], ids=["one-workgroup", "many-rows"])
+def test_index_cross_entropy_out_of_bounds_status(ctx, shape):
+    R, C = shape
     pb = ProgramBuilder()
     sx, sy = pb.input(R * C), pb.input(R, "i64")
     sl = pb.output(1)

@@ -26,6 +26,7 @@
 // gemm_nt.hip, gemm_tn.hip and gemm_tt.hip; this file holds the dispatch, the deterministic
 // split-K reduction and the K == 1 outer product.
 #include "gemm_tile.h"
+#include "gemm_v2.h"
 #include <algorithm>
 
 namespace shk {
@@ -206,6 +207,27 @@ int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K, bool colsum) {
   return floats;
 }
 
+namespace {
+// float4 loads need the contiguous extent, the leading dimension and the base aligned to 4.
+void vector_operands(const GemmParams& p, bool& va, bool& vb) {
+  const int64_t a_contig = p.transA ? p.M : p.K;
+  const int64_t b_contig = p.transB ? p.K : p.N;
+  va = a_contig % 4 == 0 && p.lda % 4 == 0 && aligned16(p.A);
+  vb = b_contig % 4 == 0 && p.ldb % 4 == 0 && aligned16(p.B);
+}
+// Whether this GEMM is split along K: problems with too few 128x128 tiles are, unless the
+// direct-to-LDS kernel can run them whole on 64x64 tiles (no partials, no reduction pass).
+bool use_split(const GemmParams& in, bool have_workspace) {
+  if (!have_workspace || in.K <= 1 || splitk_slices(in.M, in.N, in.K) <= 1) return false;
+  GemmParams p = in;
+  p.kchunk = 0;
+  p.partial = nullptr;
+  bool va, vb;
+  vector_operands(p, va, vb);
+  return !(v2_enabled() && v2_choose(p, va, vb) == 64);
+}
+}  // namespace
+
 hipError_t launch_gemm_core(const GemmParams& in, float* workspace, hipStream_t s);
 
 // Entry point: runs the GEMM and, when p.colsum is set, the column sum of the stored C -- fused
@@ -214,7 +236,7 @@ hipError_t launch_gemm(const GemmParams& in, float* workspace, hipStream_t s) {
   GemmParams p = in;
   p.colsum_partial = nullptr;
   if (p.colsum == nullptr || p.M <= 0 || p.N <= 0) return launch_gemm_core(p, workspace, s);
-  const bool split = p.K > 1 && splitk_slices(p.M, p.N, p.K) > 1;
+  const bool split = use_split(p, workspace != nullptr);
   if (p.K <= 1 || split) {
     hipError_t e = launch_gemm_core(p, workspace, s);
     if (e != hipSuccess) return e;
@@ -232,14 +254,12 @@ hipError_t launch_gemm_core(const GemmParams& in, float* workspace, hipStream_t 
   p.partial = nullptr;
   p.kchunk = 0;
   if (p.M <= 0 || p.N <= 0) return hipSuccess;
-  if (workspace != nullptr && p.K > 1 && splitk_slices(p.M, p.N, p.K) > 1) {
+  if (use_split(p, workspace != nullptr)) {
     p.kchunk = splitk_chunk(p.K, splitk_slices(p.M, p.N, p.K));
     const int slices = (int)((p.K + p.kchunk - 1) / p.kchunk);
     p.partial = workspace;
-    const int64_t a_contig = p.transA ? p.M : p.K;
-    const int64_t b_contig = p.transB ? p.K : p.N;
-    const bool va = a_contig % 4 == 0 && p.lda % 4 == 0 && aligned16(p.A);
-    const bool vb = b_contig % 4 == 0 && p.ldb % 4 == 0 && aligned16(p.B);
+    bool va, vb;
+    vector_operands(p, va, vb);
     hipError_t e = launch_tiles(p, va, vb, true, s);
     if (e != hipSuccess) return e;
     const int64_t total = p.M * p.N;
@@ -267,11 +287,8 @@ hipError_t launch_gemm_core(const GemmParams& in, float* workspace, hipStream_t 
     hipLaunchKernelGGL(gemm_k1_outer, dim3(blocks), dim3(256), 0, s, p);
     return hipGetLastError();
   }
-  // float4 loads need the contiguous extent, the leading dimension and the base aligned to 4.
-  const int64_t a_contig = p.transA ? p.M : p.K;
-  const int64_t b_contig = p.transB ? p.K : p.N;
-  const bool va = a_contig % 4 == 0 && p.lda % 4 == 0 && aligned16(p.A);
-  const bool vb = b_contig % 4 == 0 && p.ldb % 4 == 0 && aligned16(p.B);
+  bool va, vb;
+  vector_operands(p, va, vb);
   return launch_tiles(p, va, vb, false, s);
 }
 

@@ -1,27 +1,33 @@
-// Large-problem fp32 MFMA GEMM tile kernel for gfx950: 128x128 output tiles, BK = 32, four
-// waves of 64x64, v_mfma_f32_16x16x4_f32, operands moved from HBM straight into LDS.
+// Direct-to-LDS fp32 MFMA GEMM tile kernel for gfx950: BT x BT output tiles (BT = 128 or 64),
+// BK = 32, four waves of (BT/2) x (BT/2), v_mfma_f32_16x16x4_f32, operands moved from HBM straight
+// into LDS.
 //
-// Used when M and N are multiples of 128, K a multiple of 32, both operands allow 16-byte
-// loads and the problem has at least 256 output tiles (the MLP-4096 and C2-sized GEMMs); every
-// other case runs the register-staged kernel in gemm_tile.h. The epilogues are the same: bias +
-// activation, activation gradient, accumulate, the binary64 column-sum partials of a bias
+// Used when both operands allow 16-byte loads, K and N are multiples of 4 and the problem gives
+// enough workgroups (see v2_choose); ragged M / N / K edges are handled by the TAIL variants.
+// Every other case runs the register-staged kernel in gemm_tile.h. The epilogues are the same:
+// bias + activation, activation gradient, accumulate, the binary64 column-sum partials of a bias
 // gradient, and the staged optimizer update of a weight gradient.
 //
 // Data movement:
 //   * global_load_lds_dwordx4: each lane copies 16 bytes from HBM to LDS without passing through
 //     VGPRs; one wave instruction fills 1 KB of LDS. The lane -> address assignment inside an
-//     instruction is free, which is used to lay the tile out swizzled (below). Two LDS stages,
-//     software-pipelined so that fragment reads overlap MFMAs and each copy has a whole k-tile
-//     of MFMA work to land; one barrier per 32-deep k-tile (see the main loop).
+//     instruction is free, which is used to lay the tile out swizzled (gemm_v2_layout.h). Two LDS
+//     stages, software-pipelined so that fragment reads overlap MFMAs and each copy has a whole
+//     k-tile of MFMA work to land; one barrier per 32-deep k-tile (see the main loop).
 //   * K-contiguous operands (A = X[M,K], B = W[N,K]) are kept [row][k] with 16-byte chunks
 //     XOR-swizzled across each 256-byte pair of rows, so that one ds_read_b128 per lane fetches
 //     four k values of a row and the 64 lanes of a read hit 64 distinct banks.
 //   * M/N-contiguous operands (dZ^T, X, W in [K,N]) are kept [k][row] with chunks swizzled by
 //     (k / 4) mod 4; fragments are ds_read_b32.
+//   * Edges (TAIL): a lane whose 16-byte chunk lies outside the operand (row >= M or N, k >= K)
+//     skips its copy and stores zeros into that LDS chunk instead, so no load leaves the operand
+//     and the missing products are exact zeros; the epilogue stores only rows < M, columns < N.
 // Reduction order: within a 32-deep k-tile, MFMA s of half h takes k = 16h + 4g + s from lane
 // group g; the sum over k is a permutation of the straight order, which the matrix cores
 // reassociate anyway (the reference contract allows it, foundational-modules.md:423-425).
 #pragma once
+#include <cstdlib>
+
 #include "gemm_tile.h"
 #include "gemm_v2_layout.h"
 
@@ -30,55 +36,80 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int V2_BM = 128, V2_BN = 128, V2_BK = 32, V2_NT = 256;
-constexpr int V2_TILE = 128 * 32;  // floats per operand per stage
+constexpr int V2_BK = 32, V2_NT = 256;
 
-// Per-lane source offsets (bytes, relative to the tile origin) of the four 16-byte copies this
-// thread issues per operand per k-tile, and where they land.
-template <bool KMAJ>
+template <int BT>
+struct V2Cfg {
+  static constexpr int NB = BT / 32;      // 16x16 blocks per wave and dimension
+  static constexpr int WT = BT / 2;       // wave tile edge
+  static constexpr int TILEF = BT * 32;   // floats per operand per stage
+  static constexpr int NI = BT / 32;      // copies per thread per operand per k-tile
+  static constexpr int CPR = BT / 4;      // 16-byte chunks per k-row of an M/N-contiguous tile
+  static constexpr int NG = NB * NB / 2;  // groups of 8 MFMAs per half k-tile
+  static constexpr int RPG = 4 * NB / NG;  // fragment reads (blocks) issued after a group
+  static constexpr int CPG = 4 * NI / NG;  // copies issued after a group
+  static constexpr int ECPR = WT / 4;     // 16-byte chunks per row of the epilogue transpose
+};
+
+// Per-lane source offsets (bytes, relative to the tile origin) of the NI 16-byte copies this
+// thread issues per operand per k-tile, where they land, and (TAIL) the chunk's coordinates.
+template <bool KMAJ, int BT, bool TAIL>
 struct V2Loader {
-  uint32_t voff[4];
-  uint32_t wdst;  // this wave's byte offset inside a stage (wave-uniform)
+  using Cfg = V2Cfg<BT>;
+  uint32_t voff[Cfg::NI];
+  int vrow[Cfg::NI], vk[Cfg::NI];  // first row (M/N) and first k of the chunk in the tile
+  uint32_t wdst;                   // this wave's byte offset inside a stage (wave-uniform)
   __device__ __forceinline__ void init(int64_t ld) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     wdst = __builtin_amdgcn_readfirstlane((uint32_t)w * 1024u);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < Cfg::NI; ++i) {
       const int q = (i * 4 + w) * 64 + lane;  // destination chunk of this lane
       if constexpr (KMAJ) {
         const int src = v2_kmaj_src(q), r = src >> 3, c = src & 7;
         voff[i] = (uint32_t)((r * ld + 4 * c) * 4);
+        vrow[i] = r;
+        vk[i] = 4 * c;
       } else {
-        const int src = v2_mnmaj_src(q), k = src >> 5, c = src & 31;
+        const int src = v2_mnmaj_src(q, Cfg::CPR), k = src / Cfg::CPR, c = src % Cfg::CPR;
         voff[i] = (uint32_t)((k * ld + 4 * c) * 4);
+        vrow[i] = 4 * c;
+        vk[i] = k;
       }
     }
   }
   // Copy I of this wave for the k-tile whose element (row 0, k 0) is `tile`, into stage `lds`:
   // global_load_lds_dwordx4 with the tile origin in SGPRs, a per-lane 32-bit offset and the LDS
-  // destination in M0.
-  // Written as inline assembly so that the compiler does not track the copies (it would make
-  // every LDS read wait for all copies in flight, including those into the other stage); the
-  // kernel waits for them itself (v2_wait_all) before each barrier.
+  // destination in M0. Written as inline assembly so that the compiler does not track the copies
+  // (it would make every LDS read wait for all copies in flight, including those into the other
+  // stage); the kernel waits for them itself (v2_wait_all) before each barrier.
+  // TAIL: rows_left / k_left bound the valid part of the tile; other lanes store zeros.
   template <int I>
-  __device__ __forceinline__ void issue(const float* tile, float* lds) const {
+  __device__ __forceinline__ void issue(const float* tile, float* lds, int rows_left,
+                                        int k_left) const {
     const uint32_t dst =
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)lds + I * 4096u + wdst;
-    asm volatile("global_load_lds_dwordx4 %0, %1"
-                 :
-                 : "v"(voff[I]), "s"(tile), "{m0}"(dst)
-                 : "memory");
+    if (!TAIL || (vrow[I] < rows_left && vk[I] < k_left)) {
+      asm volatile("global_load_lds_dwordx4 %0, %1"
+                   :
+                   : "v"(voff[I]), "s"(tile), "{m0}"(dst)
+                   : "memory");
+    } else {
+      const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+      *reinterpret_cast<floatx4*>(lds + (I * 4 + w) * 256 + lane * 4) = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
   }
 };
 
 // Fragments of one operand for one half (16 k) of a k-tile: f[b][s] is the value lane
 // (row 16b + lane % 16 of the wave's sub-tile; group g = lane / 16) supplies to MFMA s.
-template <bool KMAJ>
+template <bool KMAJ, int BT>
 struct V2Frag {
-  floatx4 f[4];
+  floatx4 f[V2Cfg<BT>::NB];
   // K-contiguous: base[0] / base[1] are the offsets of this lane's chunk (4H + g) in the wave's
   // rows 0..15 / 16..31; blocks 2 and 3 repeat them 32 rows (1024 floats) further.
-  // M/N-contiguous: base[b] = 512 g + 64 w + 16 (b ^ g) + l16; the k-row is compile-time.
+  // M/N-contiguous: base[b] is the offset of (k = 4g, row 16b + l16); the k-row 16H + 4g + s
+  // adds (16H + s) * BT (the swizzle depends on (k / 4) mod 4 = g only).
   template <int H, int B>
   __device__ __forceinline__ void load_block(const float* lds, const int* base) {
     if constexpr (KMAJ) {
@@ -86,13 +117,13 @@ struct V2Frag {
     } else {
       static_for<4>([&](auto s) {
         constexpr int S = decltype(s)::value;
-        f[B][S] = lds[base[B] + (16 * H + S) * 128];
+        f[B][S] = lds[base[B] + (16 * H + S) * BT];
       });
     }
   }
   template <int H>
   __device__ __forceinline__ void load(const float* lds, const int* base) {
-    static_for<4>([&](auto b) { load_block<H, decltype(b)::value>(lds, base); });
+    static_for<V2Cfg<BT>::NB>([&](auto b) { load_block<H, decltype(b)::value>(lds, base); });
   }
 };
 
@@ -109,21 +140,25 @@ __device__ __forceinline__ void v2_barrier() {
 
 // The tile kernel. KA: A(m, k) is contiguous along k (A stored [M,K]); KB: B(n, k) is contiguous
 // along k (B stored [N,K]).
-template <bool KA, bool KB>
+template <bool KA, bool KB, int BT, bool TAIL>
 __global__ void __launch_bounds__(V2_NT) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_f32_v2(GemmParams p) {
-  __shared__ __attribute__((aligned(16))) float As0[V2_TILE];
-  __shared__ __attribute__((aligned(16))) float Bs0[V2_TILE];
-  __shared__ __attribute__((aligned(16))) float As1[V2_TILE];
-  __shared__ __attribute__((aligned(16))) float Bs1[V2_TILE];
+  using Cfg = V2Cfg<BT>;
+  constexpr int NB = Cfg::NB, WT = Cfg::WT, TILEF = Cfg::TILEF, NI = Cfg::NI, NG = Cfg::NG;
+  __shared__ __attribute__((aligned(16))) float As0[TILEF];
+  __shared__ __attribute__((aligned(16))) float Bs0[TILEF];
+  __shared__ __attribute__((aligned(16))) float As1[TILEF];
+  __shared__ __attribute__((aligned(16))) float Bs1[TILEF];
 
-  const int tilesM = (int)(p.M / V2_BM), tilesN = (int)(p.N / V2_BN);
+  const int tilesM = (int)((p.M + BT - 1) / BT), tilesN = (int)((p.N + BT - 1) / BT);
   int tm, tn;
   tile_of(blockIdx.x, tilesM, tilesN, tm, tn);
-  const int64_t m0 = (int64_t)tm * V2_BM, n0 = (int64_t)tn * V2_BN;
+  const int64_t m0 = (int64_t)tm * BT, n0 = (int64_t)tn * BT;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int l16 = lane & 15, g = lane >> 4;
+  const int rows_a = (int)std::min<int64_t>(BT, p.M - m0);
+  const int rows_b = (int)std::min<int64_t>(BT, p.N - n0);
 
   // operand tile origins at k = 0, and the per-k-tile advance
   // split-K: block row y covers k in [y * kchunk, min(K, (y + 1) * kchunk))
@@ -133,62 +168,69 @@ gemm_f32_v2(GemmParams p) {
   const float* b_tile = KB ? p.B + n0 * p.ldb + k_begin : p.B + n0 + k_begin * p.ldb;
   const int64_t a_step = KA ? V2_BK : V2_BK * p.lda;
   const int64_t b_step = KB ? V2_BK : V2_BK * p.ldb;
-  V2Loader<KA> la;
-  V2Loader<KB> lb;
+  V2Loader<KA, BT, TAIL> la;
+  V2Loader<KB, BT, TAIL> lb;
   la.init(p.lda);
   lb.init(p.ldb);
 
   // lane-dependent fragment offsets per half
-  int a_base[2][4], b_base[2][4];
+  int a_base[2][NB], b_base[2][NB];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      a_base[h][q] = KA ? v2_kmaj_off(wm * 64 + 16 * (q & 1) + l16, 4 * h + g)
-                        : 512 * g + 64 * wm + 16 * (q ^ g) + l16;
-      b_base[h][q] = KB ? v2_kmaj_off(wn * 64 + 16 * (q & 1) + l16, 4 * h + g)
-                        : 512 * g + 64 * wn + 16 * (q ^ g) + l16;
+    for (int q = 0; q < NB; ++q) {
+      a_base[h][q] = KA ? v2_kmaj_off(wm * WT + 16 * (q & 1) + l16, 4 * h + g)
+                        : v2_mnmaj_off(4 * g, wm * WT + 16 * q + l16, Cfg::CPR);
+      b_base[h][q] = KB ? v2_kmaj_off(wn * WT + 16 * (q & 1) + l16, 4 * h + g)
+                        : v2_mnmaj_off(4 * g, wn * WT + 16 * q + l16, Cfg::CPR);
     }
   }
 
-  floatx4 acc[4][4];
-  static_for<4>([&](auto i) {
-    static_for<4>([&](auto j) {
+  floatx4 acc[NB][NB];
+  static_for<NB>([&](auto i) {
+    static_for<NB>([&](auto j) {
       acc[decltype(i)::value][decltype(j)::value] = floatx4{0.f, 0.f, 0.f, 0.f};
     });
   });
 
-  const int nk = (int)(k_len / V2_BK);
-  // 64 MFMAs of one half-tile in 8 groups of 8 (group q: MFMA s = q / 2 of blocks
-  // i = 2 (q % 2) .. +1, j = 0..3); after each group, side(q) issues that group's share of the
+  const int nk = (int)((k_len + V2_BK - 1) / V2_BK);
+  // 4 NB^2 MFMAs of one half-tile in NG groups of 8 (MFMA n: s = n / NB^2, block
+  // i = (n % NB^2) / NB, j = n % NB); after each group, side(q) issues that group's share of the
   // LDS reads and copies. The scheduling barriers keep this order: reads and copies spread over
   // the MFMA stream instead of stalling it in one place.
-  auto mfma_half = [&](const V2Frag<KA>& fa, const V2Frag<KB>& fb, auto side) {
-    static_for<8>([&](auto q) {
-      constexpr int Q = decltype(q)::value, S = Q >> 1, I0 = 2 * (Q & 1);
-      static_for<2>([&](auto ii) {
-        static_for<4>([&](auto j) {
-          constexpr int I = I0 + decltype(ii)::value, J = decltype(j)::value;
-          acc[I][J] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa.f[I][S], fb.f[J][S], acc[I][J], 0,
-                                                          0, 0);
-        });
+  auto mfma_half = [&](const V2Frag<KA, BT>& fa, const V2Frag<KB, BT>& fb, auto side) {
+    static_for<NG>([&](auto q) {
+      constexpr int Q = decltype(q)::value;
+      static_for<8>([&](auto u) {
+        constexpr int N = 8 * Q + decltype(u)::value;
+        constexpr int S = N / (NB * NB), I = (N % (NB * NB)) / NB, J = N % NB;
+        acc[I][J] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa.f[I][S], fb.f[J][S], acc[I][J], 0, 0,
+                                                        0);
       });
       __builtin_amdgcn_sched_barrier(0);
       side(q);
       __builtin_amdgcn_sched_barrier(0);
     });
   };
-  // Fragment reads of half H from stage (As, Bs), two blocks per call for q = 0..3, ordered so
-  // that the blocks the next half's first MFMAs use come first.
-  auto read_share = [&](auto q, V2Frag<KA>& fa, V2Frag<KB>& fb, const float* As,
-                        const float* Bs, auto h) {
-    constexpr int Q = decltype(q)::value, H = decltype(h)::value;
-    const int* ab = a_base[H];
-    const int* bb = b_base[H];
-    if constexpr (Q == 0) { fa.template load_block<H, 0>(As, ab); fb.template load_block<H, 0>(Bs, bb); }
-    if constexpr (Q == 1) { fb.template load_block<H, 1>(Bs, bb); fa.template load_block<H, 1>(As, ab); }
-    if constexpr (Q == 2) { fb.template load_block<H, 2>(Bs, bb); fb.template load_block<H, 3>(Bs, bb); }
-    if constexpr (Q == 3) { fa.template load_block<H, 2>(As, ab); fa.template load_block<H, 3>(As, ab); }
+  // Fragment reads of half H from stage (As, Bs): read item t (t < 2 NB) in the order
+  // A0, B0, B1, A1, B2, B3, A2, A3, so that the blocks the next half's first MFMAs use come
+  // first; group q issues items q RPG .. q RPG + RPG - 1.
+  auto read_item = [&](auto t, V2Frag<KA, BT>& fa, V2Frag<KB, BT>& fb, const float* As,
+                       const float* Bs, auto h) {
+    constexpr int T = decltype(t)::value, H = decltype(h)::value;
+    constexpr int ORDER_OP[8] = {0, 1, 1, 0, 1, 1, 0, 0};
+    constexpr int ORDER_BLK[8] = {0, 0, 1, 1, 2, 3, 2, 3};
+    if constexpr (ORDER_OP[T] == 0) fa.template load_block<H, ORDER_BLK[T]>(As, a_base[H]);
+    else fb.template load_block<H, ORDER_BLK[T]>(Bs, b_base[H]);
+  };
+  // Copies of a k-tile: item c (c < 2 NI) is operand c % 2, instruction c / 2.
+  auto copy_item = [&](auto c, const float* at, const float* bt, float* As, float* Bs, int k_left) {
+    constexpr int C = decltype(c)::value;
+    if constexpr (C % 2 == 0) la.template issue<C / 2>(at, As, rows_a, k_left);
+    else lb.template issue<C / 2>(bt, Bs, rows_b, k_left);
+  };
+  auto copy_all = [&](const float* at, const float* bt, float* As, float* Bs, int k_left) {
+    static_for<2 * NI>([&](auto c) { copy_item(c, at, bt, As, Bs, k_left); });
   };
 
   // Software pipeline over k-tiles (tile kt lives in stage kt % 2; fa0 / fb0 hold its first-half
@@ -197,21 +239,23 @@ gemm_f32_v2(GemmParams p) {
   //   wait for this wave's copies and reads, barrier: tile kt+1 has landed everywhere and every
   //   wave has read all of tile kt;
   //   second half: MFMAs with fa1 / fb1 while tile kt+1's first-half fragments load into
-  //   fa0 / fb0 (groups 0-3) and tile kt+2 is copied into tile kt's stage (groups 4-7).
+  //   fa0 / fb0 (first half of the groups) and tile kt+2 is copied into tile kt's stage (second
+  //   half of the groups).
   // Each copy has most of a k-tile of MFMA work to land; no LDS read touches a stage while a
   // copy into it is in flight.
-  V2Frag<KA> fa0, fa1;
-  V2Frag<KB> fb0, fb1;
-  auto issue_all = [&](const float* at, const float* bt, float* As, float* Bs) {
-    la.template issue<0>(at, As); la.template issue<1>(at, As);
-    la.template issue<2>(at, As); la.template issue<3>(at, As);
-    lb.template issue<0>(bt, Bs); lb.template issue<1>(bt, Bs);
-    lb.template issue<2>(bt, Bs); lb.template issue<3>(bt, Bs);
-  };
-  issue_all(a_tile, b_tile, As0, Bs0);
+  V2Frag<KA, BT> fa0, fa1;
+  V2Frag<KB, BT> fb0, fb1;
+  copy_all(a_tile, b_tile, As0, Bs0, (int)k_len);
   if (nk > 1) {
-    issue_all(a_tile + a_step, b_tile + b_step, As1, Bs1);
-    __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): the first tile's eight copies have landed
+    copy_all(a_tile + a_step, b_tile + b_step, As1, Bs1, (int)(k_len - V2_BK));
+    if constexpr (TAIL) {
+      // lanes that stored zeros have fewer copies in flight: wait for all of them
+      v2_wait_all();
+    } else {
+      // vmcnt(2 NI): the first k-tile's copies have landed
+      if constexpr (NI == 4) __builtin_amdgcn_s_waitcnt(0x0F78);
+      else __builtin_amdgcn_s_waitcnt(0x0F74);
+    }
   } else {
     v2_wait_all();
   }
@@ -227,10 +271,16 @@ gemm_f32_v2(GemmParams p) {
     const bool more = kt + 1 < nk, copy = kt + 2 < nk;
     const float* at = a_tile + (int64_t)(kt + 2) * a_step;
     const float* bt = b_tile + (int64_t)(kt + 2) * b_step;
+    const int k_left = (int)(k_len - (int64_t)(kt + 2) * V2_BK);
     __builtin_amdgcn_sched_barrier(0);
     mfma_half(fa0, fb0, [&](auto q) {
-      if constexpr (decltype(q)::value < 4)
-        read_share(q, fa1, fb1, Acur, Bcur, std::integral_constant<int, 1>{});
+      constexpr int Q = decltype(q)::value;
+      if constexpr (Q < NG / 2) {
+        static_for<Cfg::RPG>([&](auto r) {
+          read_item(std::integral_constant<int, Q * Cfg::RPG + decltype(r)::value>{}, fa1, fb1,
+                    Acur, Bcur, std::integral_constant<int, 1>{});
+        });
+      }
     });
     if (more) {
       v2_wait_all();
@@ -239,12 +289,19 @@ gemm_f32_v2(GemmParams p) {
     __builtin_amdgcn_sched_barrier(0);
     mfma_half(fa1, fb1, [&](auto q) {
       constexpr int Q = decltype(q)::value;
-      if constexpr (Q < 4) {
-        if (more) read_share(q, fa0, fb0, Aoth, Both, std::integral_constant<int, 0>{});
+      if constexpr (Q < NG / 2) {
+        if (more) {
+          static_for<Cfg::RPG>([&](auto r) {
+            read_item(std::integral_constant<int, Q * Cfg::RPG + decltype(r)::value>{}, fa0, fb0,
+                      Aoth, Both, std::integral_constant<int, 0>{});
+          });
+        }
       } else {
         if (copy) {
-          la.template issue<Q - 4>(at, Acur);
-          lb.template issue<Q - 4>(bt, Bcur);
+          static_for<Cfg::CPG>([&](auto c) {
+            copy_item(std::integral_constant<int, (Q - NG / 2) * Cfg::CPG + decltype(c)::value>{},
+                      at, bt, Acur, Bcur, k_left);
+          });
         }
       }
     });
@@ -257,50 +314,60 @@ gemm_f32_v2(GemmParams p) {
   if (kt < nk) step(std::integral_constant<int, 0>{}, kt);
 
   // Epilogue. Accumulator r of block (i, j) holds row 16i + 4g + r, column 16j + l16 of the
-  // wave's 64x64 sub-tile. Split-K partials are written from that layout directly; otherwise
-  // the sub-tile is transposed through this wave's own 16 KB of LDS (row-major, 16-byte chunks
-  // XOR-swizzled by row) so that every global access of the epilogue is a 16-byte row segment:
-  // lane (q = lane % 16, rg = lane / 16) then owns columns 4q..4q+3 of rows rg + 4t, t < 16,
-  // and each store instruction writes four full 256-byte row segments.
-  const int64_t row_w = m0 + wm * 64 + 4 * g, col_w = n0 + wn * 64 + l16;
+  // wave's WT x WT sub-tile. Split-K partials are written from that layout directly; otherwise
+  // the sub-tile is transposed through this wave's own part of the (now free) LDS stages
+  // (row-major, 16-byte chunks XOR-swizzled by row) so that every global access of the epilogue
+  // is a 16-byte row segment: lane (q = lane % ECPR, rg = lane / ECPR) owns columns 4q..4q+3 of
+  // rows rg + (64 / ECPR) t, and each store instruction covers whole WT-float row segments.
+  const int64_t row_w = m0 + wm * WT + 4 * g, col_w = n0 + wn * WT + l16;
   if (p.partial != nullptr) {
     // split-K: raw partial sums, reduced (and given the epilogue) by gemm_splitk_reduce
     float* part = p.partial + (int64_t)blockIdx.y * p.M * p.N;
-    static_for<4>([&](auto i) {
-      static_for<4>([&](auto j) {
+    static_for<NB>([&](auto i) {
+      static_for<NB>([&](auto j) {
         constexpr int I = decltype(i)::value, J = decltype(j)::value;
-        float* dst = part + (row_w + 16 * I) * p.N + col_w + 16 * J;
-        static_for<4>([&](auto r) { dst[decltype(r)::value * p.N] = acc[I][J][decltype(r)::value]; });
+        const int64_t col = col_w + 16 * J;
+        static_for<4>([&](auto r) {
+          constexpr int R = decltype(r)::value;
+          const int64_t row = row_w + 16 * I + R;
+          if (!TAIL || (row < p.M && col < p.N)) part[row * p.N + col] = acc[I][J][R];
+        });
       });
     });
     return;
   }
   v2_wait_all();
   v2_barrier();  // every wave has finished reading its fragments: the stages are free
-  float* stage = wave == 0 ? As0 : wave == 1 ? Bs0 : wave == 2 ? As1 : Bs1;
-  static_for<4>([&](auto i) {
-    static_for<4>([&](auto j) {
+  constexpr int ECPR = Cfg::ECPR, RSTEP = 64 / ECPR, PER_ARRAY = TILEF / (WT * WT);
+  const int arr = wave / PER_ARRAY;
+  float* stage = (arr == 0 ? As0 : arr == 1 ? Bs0 : arr == 2 ? As1 : Bs1) +
+                 (wave % PER_ARRAY) * (WT * WT);
+  static_for<NB>([&](auto i) {
+    static_for<NB>([&](auto j) {
       constexpr int I = decltype(i)::value, J = decltype(j)::value;
       static_for<4>([&](auto r) {
         constexpr int R = decltype(r)::value;
         const int row = 16 * I + 4 * g + R, col = 16 * J + l16;
-        stage[row * 64 + (((col >> 2) ^ (row & 15)) << 2) + (col & 3)] = acc[I][J][R];
+        stage[row * WT + (((col >> 2) ^ (row % ECPR)) << 2) + (col & 3)] = acc[I][J][R];
       });
     });
   });
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are complete
-  const int q = lane & 15, rg = lane >> 4;
+  const int q = lane % ECPR, rg = lane / ECPR;
   auto tile_row = [&](int t) -> floatx4 {
-    const int row = rg + 4 * t;
-    return *reinterpret_cast<const floatx4*>(stage + row * 64 + ((q ^ (row & 15)) << 2));
+    const int row = rg + RSTEP * t;
+    return *reinterpret_cast<const floatx4*>(stage + row * WT + ((q ^ (row % ECPR)) << 2));
   };
-  const int64_t row_e = m0 + wm * 64 + rg, col_e = n0 + wn * 64 + 4 * q;
+  const int64_t row_e = m0 + wm * WT + rg, col_e = n0 + wn * WT + 4 * q;
+  const bool col_ok = !TAIL || col_e < p.N;  // N is a multiple of 4: whole segments
   if (p.upd.pn != nullptr) {
     const GemmUpdate& u = p.upd;
     const UpdateCtx uc = update_ctx(u);
     bool ok = uc.k.ok;
-    for (int t = 0; t < 16; ++t) {
-      const int64_t e = (row_e + 4 * t) * p.N + col_e;
+    for (int t = 0; t < WT / RSTEP; ++t) {
+      const int64_t row = row_e + RSTEP * t;
+      if (TAIL && (!col_ok || row >= p.M)) continue;
+      const int64_t e = row * p.N + col_e;
       const floatx4 gv = tile_row(t);
       const floatx4 pv = *reinterpret_cast<const floatx4*>(u.p + e);
       const floatx4 mv = u.m != nullptr ? *reinterpret_cast<const floatx4*>(u.m + e) : floatx4{0.f, 0.f, 0.f, 0.f};
@@ -323,10 +390,11 @@ gemm_f32_v2(GemmParams p) {
     return;
   }
   floatx4 bias = floatx4{0.f, 0.f, 0.f, 0.f};
-  if (p.bias != nullptr) bias = *reinterpret_cast<const floatx4*>(p.bias + col_e);
+  if (p.bias != nullptr && col_ok) bias = *reinterpret_cast<const floatx4*>(p.bias + col_e);
   double cs[4] = {0.0, 0.0, 0.0, 0.0};  // fused column sums of this lane's stored values
-  for (int t = 0; t < 16; ++t) {
-    const int64_t row = row_e + 4 * t;
+  for (int t = 0; t < WT / RSTEP; ++t) {
+    const int64_t row = row_e + RSTEP * t;
+    if (TAIL && (!col_ok || row >= p.M)) continue;
     floatx4 v = tile_row(t);
     if (p.mode == 0) {
       if (p.bias != nullptr) v = floatx4{v[0] + bias[0], v[1] + bias[1], v[2] + bias[2], v[3] + bias[3]};
@@ -347,52 +415,78 @@ gemm_f32_v2(GemmParams p) {
     static_for<4>([&](auto c) { cs[decltype(c)::value] += (double)v[decltype(c)::value]; });
   }
   if (p.colsum_partial != nullptr) {
-    // lanes q + 16 rg hold the same columns: one partial row per wave
+    // lanes q + ECPR rg hold the same columns: one partial row per wave
     static_for<4>([&](auto c) {
       constexpr int C = decltype(c)::value;
-      cs[C] += __shfl_xor(cs[C], 16, 64);
-      cs[C] += __shfl_xor(cs[C], 32, 64);
+      for (int o = ECPR; o < 64; o <<= 1) cs[C] += __shfl_xor(cs[C], o, 64);
     });
-    if (rg == 0) {
+    if (rg == 0 && col_ok) {
       double* dst = p.colsum_partial + ((int64_t)tm * 2 + wm) * p.N + col_e;
       static_for<4>([&](auto c) { dst[decltype(c)::value] = cs[decltype(c)::value]; });
     }
   }
 }
 
-// Whether the large-problem kernel handles this GEMM (see the header comment): whole tiles,
-// whole 32-deep k-tiles (per split-K slice when p.kchunk > 0), 16-byte operand loads, and
-// enough workgroups to fill the chip (output tiles times slices).
-inline bool v2_eligible(const GemmParams& p, bool va, bool vb) {
-  if (!va || !vb || p.M % V2_BM != 0 || p.N % V2_BN != 0 || p.K % V2_BK != 0 || p.K < V2_BK)
-    return false;
-  if (p.kchunk > 0 && (p.kchunk % V2_BK != 0 || p.partial == nullptr)) return false;
-  // the transposed epilogue moves 16-byte row segments
+// The direct-to-LDS kernel is on unless SHK_HIP_GEMM_V2=0 (read once per process).
+inline bool v2_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("SHK_HIP_GEMM_V2");
+    return e == nullptr || atoi(e) != 0;
+  }();
+  return on;
+}
+
+// Kernel choice for a GEMM (0: none, the register-staged kernel runs it; else the tile edge).
+//   * both operands allow 16-byte loads, K and N are multiples of 4 and, for the transposed
+//     epilogue, its pointers are 16-byte aligned with leading dimensions multiples of 4;
+//   * BT = 128 when there are at least 256 such tiles (times split-K slices);
+//   * BT = 64 for problems with at least 128 64x64 tiles and K <= 2048 that are not split, in
+//     place of splitting K (no partials, no reduction pass).
+// TAIL variants run when M, N or K (or the slice) is not a whole number of tiles.
+inline int v2_choose(const GemmParams& p, bool va, bool vb) {
+  if (!va || !vb || p.K % 4 != 0 || p.N % 4 != 0 || p.K < 4) return 0;
   auto al = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; };
-  if (p.kchunk == 0) {
-    if (p.upd.pn != nullptr) {
-      const GemmUpdate& u = p.upd;
-      if (!al(u.p) || !al(u.pn) || (u.m != nullptr && (!al(u.m) || !al(u.mn))) ||
-          (u.kind != 0 && (!al(u.v) || !al(u.vn))))
-        return false;
-    } else {
-      if (!al(p.C) || p.ldc % 4 != 0 || (p.bias != nullptr && !al(p.bias))) return false;
-      if (p.mode == 1 && (!al(p.aux) || p.ldaux % 4 != 0)) return false;
-    }
+  if (p.kchunk > 0) {
+    if (p.kchunk % V2_BK != 0 || p.partial == nullptr) return 0;
+  } else if (p.upd.pn != nullptr) {
+    const GemmUpdate& u = p.upd;
+    if (!al(u.p) || !al(u.pn) || (u.m != nullptr && (!al(u.m) || !al(u.mn))) ||
+        (u.kind != 0 && (!al(u.v) || !al(u.vn))))
+      return 0;
+  } else {
+    if (!al(p.C) || p.ldc % 4 != 0 || (p.bias != nullptr && !al(p.bias))) return 0;
+    if (p.mode == 1 && (!al(p.aux) || p.ldaux % 4 != 0)) return 0;
   }
-  const int64_t tiles = (p.M / V2_BM) * (p.N / V2_BN);
+  const int64_t ld = std::max(p.lda, p.ldb);
+  if ((p.M + 128) * ld >= (1LL << 31) || (p.N + 128) * ld >= (1LL << 31) ||
+      (p.K + 128) * ld >= (1LL << 31))
+    return 0;
   const int64_t slices = p.kchunk > 0 ? (p.K + p.kchunk - 1) / p.kchunk : 1;
-  return tiles * slices >= 256 && tiles < (1LL << 31) && slices < 65536 &&
-         p.M * std::max(p.lda, p.ldb) < (1LL << 31) && p.K * std::max(p.lda, p.ldb) < (1LL << 31);
+  const int64_t t128 = ((p.M + 127) / 128) * ((p.N + 127) / 128);
+  const int64_t t64 = ((p.M + 63) / 64) * ((p.N + 63) / 64);
+  if (t64 >= (1LL << 31) || slices >= 65536) return 0;
+  if (t128 * slices >= 256) return 128;
+  if (p.kchunk == 0 && t64 >= 128 && p.K <= 2048) return 64;
+  return 0;
+}
+
+template <bool TA, bool TB, int BT>
+hipError_t launch_v2_bt(const GemmParams& p, hipStream_t s) {
+  g_colsum_rows = ((p.M + BT - 1) / BT) * 2;
+  const unsigned tiles = (unsigned)(((p.M + BT - 1) / BT) * ((p.N + BT - 1) / BT));
+  const unsigned slices = p.kchunk > 0 ? (unsigned)((p.K + p.kchunk - 1) / p.kchunk) : 1u;
+  const int64_t span = p.kchunk > 0 ? p.kchunk : p.K;
+  const bool tail = p.M % BT != 0 || p.N % BT != 0 || span % V2_BK != 0 || p.K % V2_BK != 0;
+  if (tail)
+    hipLaunchKernelGGL((gemm_f32_v2<!TA, TB, BT, true>), dim3(tiles, slices), dim3(V2_NT), 0, s, p);
+  else
+    hipLaunchKernelGGL((gemm_f32_v2<!TA, TB, BT, false>), dim3(tiles, slices), dim3(V2_NT), 0, s, p);
+  return hipGetLastError();
 }
 
 template <bool TA, bool TB>
-hipError_t launch_v2(const GemmParams& p, hipStream_t s) {
-  g_colsum_rows = (p.M / V2_BM) * 2;
-  const unsigned tiles = (unsigned)((p.M / V2_BM) * (p.N / V2_BN));
-  const unsigned slices = p.kchunk > 0 ? (unsigned)((p.K + p.kchunk - 1) / p.kchunk) : 1u;
-  hipLaunchKernelGGL((gemm_f32_v2<!TA, TB>), dim3(tiles, slices), dim3(V2_NT), 0, s, p);
-  return hipGetLastError();
+hipError_t launch_v2(const GemmParams& p, int bt, hipStream_t s) {
+  return bt == 64 ? launch_v2_bt<TA, TB, 64>(p, s) : launch_v2_bt<TA, TB, 128>(p, s);
 }
 
 }  // namespace

@@ -261,3 +261,43 @@ def test_large_tile_kernel_strided_operands_and_output(ctx):
     Z = oracle.matmul(np.ascontiguousarray(A[:, :K]), np.ascontiguousarray(B[:, :N]))
     assert np.array_equal(C[:, :N], oracle.activation_grad("relu", Z, np.ascontiguousarray(y[:, :N])))
     assert (C[:, N:] == 7.0).all()
+
+
+# Shapes for the 64x64 direct-to-LDS tiles (no split-K) and the ragged-edge (TAIL) variants:
+# whole tiles; ragged K (784 = 24.5 k-tiles); ragged N (784); ragged M, N and K together; a
+# ragged split-K problem on 128x128 tiles.
+EDGE_SHAPES = [(1024, 1024, 1024), (1024, 1024, 784), (1024, 784, 1024), (1000, 1028, 100),
+               (4100, 2052, 36), (200, 1024, 4100)]
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("shape", EDGE_SHAPES, ids=str)
+def test_direct_lds_kernel_edges_integer_bit_exact(ctx, shape, ta, tb):
+    M, N, K = shape
+    if ta and M % 4:
+        pytest.skip("M-contiguous A needs M % 4 == 0 for 16-byte loads (other kernel)")
+    rng = np.random.default_rng(M + 5 * N + 11 * K + 2 * ta + tb)
+    A = rng.integers(-3, 4, size=(K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.integers(-3, 4, size=(N, K) if tb else (K, N)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    C = _gemm_case(ctx, A, B, M, N, K, ta, tb, bias=b, act="relu")
+    Z = oracle.matmul(A, B, trans_a=ta, trans_b=tb)
+    assert np.array_equal(C, oracle.activation("relu", Z + b)), f"max diff {np.abs(C - oracle.activation('relu', Z + b)).max()}"
+
+
+@pytest.mark.parametrize("shape", [(1024, 1024, 1024), (1000, 1028, 100)], ids=str)
+def test_direct_lds_kernel_edges_gradient_column_sum(ctx, shape):
+    M, N, K = shape
+    rng = np.random.default_rng(43)
+    dZ = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    W = rng.integers(-3, 4, size=(K, N)).astype(np.float32)
+    y = oracle.activation("tanh", rng.standard_normal((M, N)).astype(np.float32))
+    pb = ProgramBuilder()
+    sa, sb, sy = pb.input(M * K), pb.input(K * N), pb.input(M * N)
+    sc, sd = pb.output(M * N), pb.output(N)
+    pb.gemm(sa, sb, sc, M, N, K, aux=sy, act="tanh", act_grad=True, colsum=sd)
+    C, db = run_program(ctx, pb, [dZ, W, y], [sc, sd])
+    C = C.reshape(M, N)
+    assert np.array_equal(C, oracle.activation_grad("tanh", oracle.matmul(dZ, W), y))
+    np.testing.assert_array_max_ulp(db, oracle.colsum(C), maxulp=1)

@@ -1,6 +1,7 @@
 """LDS layout maps of the large-problem GEMM kernel (synaptik_amd/csrc/gemm_v2_layout.h), built
 for the host: copy placement and fragment addressing are inverse bijections, the kernel's
-precomputed fragment offsets match the layout, and fragment reads are free of bank conflicts."""
+precomputed fragment offsets match the layout, and fragment reads are free of bank conflicts,
+for both tile edges (128 and 64)."""
 import shutil
 import subprocess
 from pathlib import Path

@@ -448,64 +448,6 @@ __global__ void __launch_bounds__(256) ce_grad(const float* __restrict__ logits,
   }
 }
 
-// Small problems (R <= 8192 rows of C <= 64 classes): loss and gradient in one workgroup, one
-// row per thread, so the three launches of the general path become one. Same arithmetic per row
-// (maximum by '>', binary64 sum of the binary32 addends, max + log(sum)), the loss and the count
-// summed in binary64 through the block tree.
-constexpr int CE_SMALL_NT = 1024;
-template <typename T>
-__global__ void __launch_bounds__(CE_SMALL_NT) ce_small(const float* __restrict__ logits,
-                                                        const T* __restrict__ target, int64_t R,
-                                                        int64_t C, int has_ignore, int64_t ignore,
-                                                        float g, float* loss,
-                                                        float* __restrict__ grad,
-                                                        uint32_t* status) {
-  __shared__ double dl[CE_SMALL_NT / 64];
-  double s_loss = 0.0, s_count = 0.0;
-  for (int64_t r = threadIdx.x; r < R; r += CE_SMALL_NT) {
-    const int64_t t = (int64_t)target[r];
-    if (has_ignore && t == ignore) continue;
-    if (t < 0 || t >= C) {
-      atomicOr(status, (uint32_t)DEV_INDEX_OUT_OF_BOUNDS);
-      continue;
-    }
-    const float* row = logits + r * C;
-    float m = -INFINITY;
-    for (int64_t c = 0; c < C; ++c) if (row[c] > m) m = row[c];
-    double s = 0.0;
-    for (int64_t c = 0; c < C; ++c) s += (double)(float)exp((double)(row[c] - m));
-    const float lse = m + (float)log((double)(float)s);
-    s_loss += (double)(lse - row[t]);
-    s_count += 1.0;
-  }
-  s_loss = block_sum<CE_SMALL_NT>(s_loss, dl);
-  __syncthreads();
-  s_count = block_sum<CE_SMALL_NT>(s_count, dl);
-  if (threadIdx.x == 0) loss[0] = (float)s_loss / (float)s_count;
-  if (grad == nullptr) return;
-  const float scale = g / (float)s_count;
-  for (int64_t r = threadIdx.x; r < R; r += CE_SMALL_NT) {
-    const int64_t t = (int64_t)target[r];
-    const float* row = logits + r * C;
-    float* gr = grad + r * C;
-    if (has_ignore && t == ignore) {
-      for (int64_t c = 0; c < C; ++c) gr[c] = 0.0f;
-      continue;
-    }
-    const int64_t safe = t < 0 ? 0 : (t >= C ? C - 1 : t);
-    float m = -INFINITY;
-    for (int64_t c = 0; c < C; ++c) m = java_max(m, row[c]);
-    double s = 0.0;
-    for (int64_t c = 0; c < C; ++c) s += (double)(float)exp((double)(row[c] - m));
-    const float sum = (float)s;
-    for (int64_t c = 0; c < C; ++c) {
-      const float prob = (float)exp((double)(row[c] - m)) / sum;
-      const float hot = c == safe ? 1.0f : 0.0f;
-      gr[c] = (prob - hot) * scale;
-    }
-  }
-}
-
 }  // namespace
 
 hipError_t launch_softmax_fwd(const float* x, float* y, float* lse, int64_t R, int64_t C,
@@ -569,17 +511,6 @@ hipError_t launch_index_ce(const float* logits, const void* target, int target_i
                            int64_t ignore_index, float g, double* partial, uint32_t* status,
                            hipStream_t s) {
   if (R <= 0) return hipSuccess;
-  if (R <= 8192 && C <= 64) {
-    if (target_is_64)
-      hipLaunchKernelGGL(ce_small<int64_t>, dim3(1), dim3(CE_SMALL_NT), 0, s, logits,
-                         (const int64_t*)target, R, C, has_ignore, ignore_index, g, loss, grad,
-                         status);
-    else
-      hipLaunchKernelGGL(ce_small<int32_t>, dim3(1), dim3(CE_SMALL_NT), 0, s, logits,
-                         (const int32_t*)target, R, C, has_ignore, ignore_index, g, loss, grad,
-                         status);
-    return hipGetLastError();
-  }
   const unsigned blocks = (unsigned)((R + 3) / 4);
   if (target_is_64)
     hipLaunchKernelGGL(ce_pass1<int64_t>, dim3(blocks), dim3(256), 0, s, logits,

@@ -69,7 +69,7 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restric
   for (int i = 0; i < V; ++i) {
     const int c = threadIdx.x + i * SM_NT;
     if (c < C4) {
-      v[i] = xr[c];
+      v[i] = ld_stream(&xr[c]);
       m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
       mn = fminf(mn, fminf(fminf(v[i].x, v[i].y), fminf(v[i].z, v[i].w)));
     }
@@ -172,7 +172,7 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restric
         o.z = e[i].z / sum;
         o.w = e[i].w / sum;
       }
-      yr[c] = o;
+      st_stream(&yr[c], o);
     }
   }
   if (lse != nullptr) {
@@ -255,8 +255,8 @@ __global__ void __launch_bounds__(SM_NT) softmax_bwd_regs(const float* __restric
   for (int i = 0; i < V; ++i) {
     const int c = threadIdx.x + i * SM_NT;
     if (c < C4) {
-      yv[i] = yr[c];
-      gv[i] = gr[c];
+      yv[i] = ld_stream(&yr[c]);
+      gv[i] = ld_stream(&gr[c]);
       s += (double)(gv[i].x * yv[i].x);
       s += (double)(gv[i].y * yv[i].y);
       s += (double)(gv[i].z * yv[i].z);
@@ -281,7 +281,7 @@ __global__ void __launch_bounds__(SM_NT) softmax_bwd_regs(const float* __restric
         o.z = o.z + k * yv[i].z;
         o.w = o.w + k * yv[i].w;
       }
-      dr[c] = o;
+      st_stream(&dr[c], o);
     }
   }
 }
@@ -329,7 +329,26 @@ __global__ void __launch_bounds__(256) mse_pass1(const float* __restrict__ p,
   __shared__ double dl[4];
   double s = 0.0;
   const int64_t stride = (int64_t)gridDim.x * 256;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+  const bool vec = ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(t) |
+                     reinterpret_cast<uintptr_t>(grad)) & 15u) == 0;
+  int64_t head = 0;
+  if (vec) {
+    // four elements per thread and iteration, streaming 16-byte accesses
+    const int64_t n4 = n / 4;
+    for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < n4; q += stride) {
+      const float4 pv = ld_stream(reinterpret_cast<const float4*>(p) + q);
+      const float4 tv = ld_stream(reinterpret_cast<const float4*>(t) + q);
+      const float d0 = pv.x - tv.x, d1 = pv.y - tv.y, d2 = pv.z - tv.z, d3 = pv.w - tv.w;
+      const float q0 = d0 * d0, q1 = d1 * d1, q2 = d2 * d2, q3 = d3 * d3;
+      s += ((double)q0 + (double)q1) + ((double)q2 + (double)q3);
+      if (grad != nullptr) {
+        const float t0 = d0 * 2.0f, t1 = d1 * 2.0f, t2 = d2 * 2.0f, t3 = d3 * 2.0f;
+        st_stream(reinterpret_cast<float4*>(grad) + q, make_float4(t0 * gn, t1 * gn, t2 * gn, t3 * gn));
+      }
+    }
+    head = n4 * 4;
+  }
+  for (int64_t i = head + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
     const float d = p[i] - t[i];
     const float sq = d * d;
     s += (double)sq;

@@ -76,8 +76,9 @@ __global__ void __launch_bounds__(OPT_NT) optimizer_kernel(OptParams p) {
   if (p.kind != 0) k = adam_coeffs(p, completed + 1);
   const int64_t base = ((int64_t)blockIdx.x - T.start) * OPT_CHUNK;
   bool ok = k.ok;
-  // Each thread owns 4 consecutive elements: 128-bit loads and stores when all 4 exist and every
-  // pointer is 16-byte aligned (device allocations and arena slots are), scalar otherwise.
+  // Each thread owns 4 consecutive elements: 128-bit streaming loads and stores when all 4 exist
+  // and every pointer is 16-byte aligned (device allocations and arena slots are), scalar
+  // otherwise.
   const int64_t i0 = base + (int64_t)threadIdx.x * OPT_PER_THREAD;
   const bool vec = i0 + 3 < T.n &&
       ((reinterpret_cast<uintptr_t>(T.p) | reinterpret_cast<uintptr_t>(T.g) |
@@ -87,10 +88,10 @@ __global__ void __launch_bounds__(OPT_NT) optimizer_kernel(OptParams p) {
   float pv[4], gv[4], mv[4], vv[4], pc[4], mc[4], vc[4];
   const int cnt = vec ? 4 : (int)max<int64_t>(0, min<int64_t>(4, T.n - i0));
   if (vec) {
-    *reinterpret_cast<float4*>(pv) = *reinterpret_cast<const float4*>(T.p + i0);
-    *reinterpret_cast<float4*>(gv) = *reinterpret_cast<const float4*>(T.g + i0);
-    if (T.m != nullptr) *reinterpret_cast<float4*>(mv) = *reinterpret_cast<const float4*>(T.m + i0);
-    if (p.kind != 0) *reinterpret_cast<float4*>(vv) = *reinterpret_cast<const float4*>(T.v + i0);
+    *reinterpret_cast<float4*>(pv) = ld_stream(reinterpret_cast<const float4*>(T.p + i0));
+    *reinterpret_cast<float4*>(gv) = ld_stream(reinterpret_cast<const float4*>(T.g + i0));
+    if (T.m != nullptr) *reinterpret_cast<float4*>(mv) = ld_stream(reinterpret_cast<const float4*>(T.m + i0));
+    if (p.kind != 0) *reinterpret_cast<float4*>(vv) = ld_stream(reinterpret_cast<const float4*>(T.v + i0));
   } else {
     for (int q = 0; q < cnt; ++q) {
       pv[q] = T.p[i0 + q];
@@ -117,9 +118,9 @@ __global__ void __launch_bounds__(OPT_NT) optimizer_kernel(OptParams p) {
     float* dm = p.phase == 1 ? T.m : T.mn;
     float* dv = p.phase == 1 ? T.v : T.vn;
     if (vec) {
-      *reinterpret_cast<float4*>(dp + i0) = *reinterpret_cast<const float4*>(pc);
-      if (dm != nullptr) *reinterpret_cast<float4*>(dm + i0) = *reinterpret_cast<const float4*>(mc);
-      if (p.kind != 0) *reinterpret_cast<float4*>(dv + i0) = *reinterpret_cast<const float4*>(vc);
+      st_stream(reinterpret_cast<float4*>(dp + i0), *reinterpret_cast<const float4*>(pc));
+      if (dm != nullptr) st_stream(reinterpret_cast<float4*>(dm + i0), *reinterpret_cast<const float4*>(mc));
+      if (p.kind != 0) st_stream(reinterpret_cast<float4*>(dv + i0), *reinterpret_cast<const float4*>(vc));
     } else {
       for (int q = 0; q < cnt; ++q) {
         dp[i0 + q] = pc[q];

@@ -363,8 +363,23 @@ def main() -> int:
     opt_gbs = (20.0 * n_params) / (opt_ms * 1e-3) / 1e9 if opt_ms > 0 else None
     print(f"[bench] breakdown {breakdown}; optimizer {opt_gbs:.0f} GB/s", file=sys.stderr, flush=True)
 
+    # The same step with the batch handed over as host arrays (upload over PCIe from pageable
+    # memory, objective downloaded): a reported figure, never `value`.
+    rng = np.random.default_rng(3)
+    xh = rng.standard_normal((BATCH, WIDTH), dtype=np.float32)
+    yh = rng.standard_normal((BATCH, WIDTH), dtype=np.float32)
+    sess.run(xh, yh)
+    t0 = time.perf_counter()
+    host_steps = 5
+    for _ in range(host_steps):
+        sess.run(xh, yh)
+    host_ms = (time.perf_counter() - t0) / host_steps * 1e3
+    host_batch = {"samples_per_s": round(BATCH / host_ms * 1e3, 1), "ms_per_step": round(host_ms, 3),
+                  "note": "batch uploaded from pageable host memory each step (2 x 64 MiB)"}
     sess.close()
     extra = None if args.no_secondary else secondary(ctx, cpu=args.cpu_sample > 0)
+    if extra is not None:
+        extra["c4_host_batch"] = host_batch
     if extra:
         print(f"[bench] secondary {extra}", file=sys.stderr, flush=True)
     cpu = None

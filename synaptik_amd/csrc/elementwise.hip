@@ -52,7 +52,7 @@ __device__ __forceinline__ void pw_load4(const PwParams& p, int k, int64_t e0, i
   switch (p.in_mode[k]) {
     case 0:
       if (cnt == 4 && (reinterpret_cast<uintptr_t>(src + e0) & 15u) == 0) {
-        const float4 t = *reinterpret_cast<const float4*>(src + e0);
+        const float4 t = ld_stream(reinterpret_cast<const float4*>(src + e0));
         v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
       } else {
         for (int q = 0; q < cnt; ++q) v[q] = src[e0 + q];
@@ -152,7 +152,7 @@ __global__ void __launch_bounds__(PW_NT) pointwise_kernel(PwParams p) {
       if (p.out[o] == nullptr) continue;
       float* dst = p.out[o] + e0;
       if (cnt == 4 && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
-        *reinterpret_cast<float4*>(dst) = make_float4(outv[o][0], outv[o][1], outv[o][2], outv[o][3]);
+        st_stream(reinterpret_cast<float4*>(dst), make_float4(outv[o][0], outv[o][1], outv[o][2], outv[o][3]));
       } else {
         for (int q = 0; q < cnt; ++q) dst[q] = outv[o][q];
       }

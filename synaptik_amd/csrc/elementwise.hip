@@ -204,6 +204,39 @@ __global__ void __launch_bounds__(256) colsum_pass1(const float* __restrict__ x,
   if (w == 0 && col < N)
     part[(int64_t)blockIdx.y * N + col] = ((lds[0][lane] + lds[1][lane]) + lds[2][lane]) + lds[3][lane];
 }
+// Pass 1 for 16-byte-aligned rows (N and ldx multiples of 4, x 16-byte aligned): each lane owns
+// four adjacent columns and reads them with one streaming 16-byte load per row, so a wave moves
+// 1 KiB per row and a block covers 256 columns. Panels, row assignment (rows r0 + w, r0 + w + 4,
+// ...) and the combination order are those of colsum_pass1, so both write identical partials.
+__global__ void __launch_bounds__(256) colsum_pass1_v4(const float* __restrict__ x, double* part,
+                                                      int64_t R, int64_t N, int64_t ldx,
+                                                      int64_t rows) {
+  __shared__ double lds[4][4 * CS_COLS];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t col = ((int64_t)blockIdx.x * CS_COLS + lane) * 4;
+  const int64_t r0 = (int64_t)blockIdx.y * rows;
+  double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+  if (col < N) {
+    const int64_t rend = min<int64_t>(R, r0 + rows);
+#pragma unroll 4
+    for (int64_t r = r0 + w; r < rend; r += 4) {
+      const float4 v = ld_stream(reinterpret_cast<const float4*>(x + r * ldx + col));
+      s0 += (double)v.x;
+      s1 += (double)v.y;
+      s2 += (double)v.z;
+      s3 += (double)v.w;
+    }
+  }
+  lds[w][4 * lane + 0] = s0;
+  lds[w][4 * lane + 1] = s1;
+  lds[w][4 * lane + 2] = s2;
+  lds[w][4 * lane + 3] = s3;
+  __syncthreads();
+  const int c = threadIdx.x;  // one column of the block's 256 per thread
+  const int64_t gc = (int64_t)blockIdx.x * 4 * CS_COLS + c;
+  if (gc < N)
+    part[(int64_t)blockIdx.y * N + gc] = ((lds[0][c] + lds[1][c]) + lds[2][c]) + lds[3][c];
+}
 // Column sums, pass 2: block x finishes 64 columns; wave w adds partial rows w, w + 4, ... in
 // two interleaved chains (independent loads in flight), then the chains and the four waves are
 // combined in a fixed order, so results are run-to-run identical.
@@ -370,8 +403,13 @@ hipError_t launch_colsum(const float* x, float* out, int64_t R, int64_t N, int64
   const int64_t rows = colsum_rows_per_panel(R, N);
   const int64_t P = (R + rows - 1) / rows;
   if (P > 0) {
-    dim3 g1((unsigned)((N + CS_COLS - 1) / CS_COLS), (unsigned)P);
-    hipLaunchKernelGGL(colsum_pass1, g1, dim3(256), 0, s, x, partial, R, N, ldx, rows);
+    if (N % 4 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+      dim3 g1((unsigned)((N + 4 * CS_COLS - 1) / (4 * CS_COLS)), (unsigned)P);
+      hipLaunchKernelGGL(colsum_pass1_v4, g1, dim3(256), 0, s, x, partial, R, N, ldx, rows);
+    } else {
+      dim3 g1((unsigned)((N + CS_COLS - 1) / CS_COLS), (unsigned)P);
+      hipLaunchKernelGGL(colsum_pass1, g1, dim3(256), 0, s, x, partial, R, N, ldx, rows);
+    }
   }
   hipLaunchKernelGGL(colsum_pass2, dim3((unsigned)((N + CS_COLS - 1) / CS_COLS)), dim3(256), 0, s,
                      partial, out, P, N, divisor, accumulate);

@@ -97,7 +97,7 @@ def test_pointwise_activation_forward_and_grad(ctx, act):
 
 
 # ---- reductions ----
-@pytest.mark.parametrize("R,N", [(1, 1), (4096, 4096), (1000, 10), (8192, 1024), (3, 70000)])
+@pytest.mark.parametrize("R,N", [(1, 1), (4096, 4096), (1000, 10), (8192, 1024), (3, 70000), (517, 12), (1025, 1284)])
 def test_colsum_against_exact_oracle(ctx, R, N):
     rng = np.random.default_rng(R + N)
     x = rng.standard_normal((R, N)).astype(np.float32)

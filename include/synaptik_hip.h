@@ -98,6 +98,38 @@ int32_t shk_hip_buffer_download_canonical(void* buffer, uint32_t element_width, 
                                           void* destination, uint64_t destination_capacity,
                                           uint64_t maximum_bytes);
 
+/* Storage-layout transfers: the physical referenced span of a typed view, moved byte for byte
+ * between host memory and a device buffer of exactly that size (prefix and gap bytes included,
+ * uninterpreted). Replace the Metal sides of the prepared CPU/device buffer transfer
+ * (MetalBackendRuntime.acceptsStorageLayoutTransfer / bindStorageLayoutUpload /
+ * bindStorageLayoutDownload, MetalBackendRuntime.java:211-281, used by
+ * CpuMetalPreparedBufferTransfer.java:185-249). The geometry must be a storage transfer
+ * (MetalBackendRuntime.isStorageTransfer, :433-478): rank 0..16, every extent and stride
+ * positive (strides NULL = dense row-major), the axes with extent > 1 sorted by stride each
+ * starting at or beyond the span the smaller ones cover (no overlap), span = storage_offset +
+ * covered elements, and span * element_width representable as a positive int64.
+ *
+ * shk_hip_storage_transfer_bytes writes that byte extent to *out_bytes, or 0 when the geometry
+ * is not a storage transfer; it touches no device. */
+int32_t shk_hip_storage_transfer_bytes(uint32_t element_width, uint32_t rank, const int64_t* dims,
+                                       const int64_t* strides, int64_t storage_offset,
+                                       uint64_t* out_bytes);
+/* Host -> device. INVALID_ARGUMENT when the geometry is not a storage transfer, the buffer's
+ * byte size differs from the extent, or source_bytes is smaller than it; boolean != 0 (BOOL,
+ * element_width 1): every logical element of the source must be 0 or 1, checked on the host
+ * before anything is copied. Synchronous. */
+int32_t shk_hip_buffer_upload_storage(void* buffer, uint32_t element_width, int32_t boolean,
+                                      uint32_t rank, const int64_t* dims, const int64_t* strides,
+                                      int64_t storage_offset, const void* source,
+                                      uint64_t source_bytes);
+/* Device -> host, same checks with destination_capacity. For BOOL every logical element is
+ * validated on the device first; on a non-canonical byte the call fails with INVALID_ARGUMENT
+ * and the destination is not written. Synchronous. */
+int32_t shk_hip_buffer_download_storage(void* buffer, uint32_t element_width, int32_t boolean,
+                                        uint32_t rank, const int64_t* dims,
+                                        const int64_t* strides, int64_t storage_offset,
+                                        void* destination, uint64_t destination_capacity);
+
 /* Programs: an op-list image (the HIP analogue of the Metal graph image decoded by
  * synaptik_metal_mpsgraph_executable_create, synaptik_metal_foundation.m:8573). The program
  * owns a device arena for its internal slots and scratch, allocated once here and reused by

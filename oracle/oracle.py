@@ -261,6 +261,64 @@ def canonical_bytes(raw: bytes, width: int, shape, strides=None, offset: int = 0
     return dst.tobytes()[:count * w]
 
 
+_LONG_MIN, _LONG_MAX = -(1 << 63), (1 << 63) - 1
+
+
+def _exact(v: int) -> int:
+    """Java Math.*Exact: a result outside the signed 64-bit range throws ArithmeticException."""
+    if not _LONG_MIN <= v <= _LONG_MAX:
+        raise ArithmeticError("long overflow")
+    return v
+
+
+def storage_transfer_bytes(width: int, shape, strides, offset: int) -> int:
+    """Byte extent of a prepared storage-layout transfer, or 0 when the view is not one.
+
+    Restates MetalBackendRuntime.isStorageTransfer / transferByteCount
+    (modules/backend/metal/.../MetalBackendRuntime.java:425-484) and
+    CpuMetalPreparedBufferTransfer.transferByteCount (modules/engine/.../
+    CpuMetalPreparedBufferTransfer.java:79-127): rank <= 16, every extent and stride > 0, the
+    axes of extent > 1 insertion-sorted by stride (only a strictly larger stride moves ahead),
+    each stride >= the span covered so far (covered starts at 1 and grows by (extent - 1) *
+    stride), referencedElementSpan = offset + covered (LayoutGeometry.referencedElementSpan for a
+    non-empty view), and span * width a positive long. Any Math.*Exact overflow rejects.
+    `strides` None is the contiguous row-major layout (LayoutDescriptor.contiguous)."""
+    shape = [int(d) for d in shape]
+    if len(shape) > 16 or width not in (1, 2, 4, 8) or offset < 0:
+        return 0
+    if strides is None:
+        strides, e = [0] * len(shape), 1
+        for a in range(len(shape) - 1, -1, -1):
+            strides[a] = e
+            e *= max(shape[a], 1)
+    strides = [int(x) for x in strides]
+    act_s, act_d = [], []
+    try:
+        for d, st in zip(shape, strides):
+            if d <= 0 or st <= 0:
+                return 0
+            _exact(d)
+            _exact(st)
+            if d > 1:
+                i = len(act_s)
+                act_s.append(st)
+                act_d.append(d)
+                while i > 0 and act_s[i - 1] > st:
+                    act_s[i], act_d[i] = act_s[i - 1], act_d[i - 1]
+                    i -= 1
+                act_s[i], act_d[i] = st, d
+        covered = 1
+        for st, d in zip(act_s, act_d):
+            if st < covered:
+                return 0
+            covered = _exact(covered + _exact((d - 1) * st))
+        span = _exact(int(offset) + covered)
+        nbytes = _exact(span * width)
+    except ArithmeticError:
+        return 0
+    return nbytes if nbytes > 0 else 0
+
+
 class OracleMLP:
     """Fully-connected network with per-layer activations; weights W[out,in], biases [out].
 

@@ -35,7 +35,7 @@ from typing import Optional, Sequence
 
 import numpy as np
 
-from .native import HipBuffer, HipContext, HipProgram
+from .native import HipBuffer, HipContext, HipProgram, storage_transfer_bytes
 from .program import ProgramBuilder, Slot
 
 BACKEND_ID = "hip"
@@ -66,6 +66,8 @@ class TensorDescriptor:
     shape: tuple
     strides: Optional[tuple] = None
     storage_offset: int = 0
+    # False: the layout is not resolved yet (Optional.empty() in TensorDescriptor.layout())
+    layout_resolved: bool = True
 
     @property
     def count(self) -> int:
@@ -280,6 +282,18 @@ class HipPreparedExecutable:
         self.program.close()
 
 
+def storage_transfer_extent(descriptor: TensorDescriptor) -> int:
+    """Physical byte extent of a storage-layout transfer of `descriptor`, 0 when it is not one:
+    unresolved layout, FP8, or a geometry MetalBackendRuntime.isStorageTransfer
+    (MetalBackendRuntime.java:429-478) rejects. Computed by the native library's host code."""
+    if descriptor is None:
+        raise TypeError("descriptor must not be None")
+    if not descriptor.layout_resolved or descriptor.dtype not in STORAGE_WIDTH:
+        return 0
+    return storage_transfer_bytes(STORAGE_WIDTH[descriptor.dtype], descriptor.shape,
+                                  descriptor.strides, descriptor.storage_offset)
+
+
 class HipBackendIntegration:
     """HipBackendIntegration.open(config): context + SPI roles (MetalBackendIntegration.java:50-103)."""
 
@@ -345,8 +359,130 @@ class HipBackendIntegration:
                                          boolean=descriptor.dtype == "BOOL",
                                          maximum_bytes=maximum_bytes)
 
+    # ---- prepared storage-layout transfers (MetalBackendIntegration.java:200-265) ----
+    def storage_transfer_extent(self, descriptor: TensorDescriptor) -> int:
+        return storage_transfer_extent(descriptor)
+
+    def accepts_storage_layout_transfer(self, buffer: HipBuffer,
+                                        descriptor: TensorDescriptor) -> bool:
+        """Whether `buffer` is a live buffer of this context whose byte size is exactly the
+        transfer extent of `descriptor` (MetalBackendRuntime.acceptsStorageLayoutTransfer,
+        MetalBackendRuntime.java:211-223)."""
+        if buffer is None or descriptor is None:
+            raise TypeError("representation and descriptor must not be None")
+        extent = self.storage_transfer_extent(descriptor)
+        return (extent > 0 and isinstance(buffer, HipBuffer) and buffer.ctx is self.context
+                and bool(buffer.handle) and buffer.nbytes == extent)
+
+    def _transfer_args(self, buffer, descriptor, what):
+        if not self.accepts_storage_layout_transfer(buffer, descriptor):
+            raise ValueError(f"HIP {what} requires an exact live storage representation")
+        return (STORAGE_WIDTH[descriptor.dtype], descriptor.shape, descriptor.strides,
+                descriptor.storage_offset, descriptor.dtype == "BOOL")
+
+    def bind_storage_layout_upload(self, buffer: HipBuffer, descriptor: TensorDescriptor):
+        """Cold-binds `buffer` as the destination of a physical storage-layout upload
+        (MetalBackendRuntime.bindStorageLayoutUpload, MetalBackendRuntime.java:233-247). The
+        returned action takes host storage of at least the extent; BOOL logical elements are
+        validated before the device is written."""
+        width, shape, strides, offset, boolean = self._transfer_args(buffer, descriptor, "upload")
+
+        def upload(source: np.ndarray) -> None:
+            buffer.upload_storage(width, shape, strides, offset, source, boolean=boolean)
+        return upload
+
+    def bind_storage_layout_download(self, buffer: HipBuffer, descriptor: TensorDescriptor):
+        """Cold-binds `buffer` as the source of a physical storage-layout download
+        (MetalBackendRuntime.bindStorageLayoutDownload, MetalBackendRuntime.java:260-281): the
+        action writes the whole span into writable host storage; a BOOL view is validated on the
+        device first and a non-canonical byte leaves the destination untouched."""
+        width, shape, strides, offset, boolean = self._transfer_args(buffer, descriptor, "download")
+
+        def download(destination: np.ndarray) -> None:
+            buffer.download_storage(width, shape, strides, offset, destination, boolean=boolean)
+        return download
+
     def close(self):
         self.context.close()
+
+
+class BoundBufferTransfer:
+    """One bound per-run transfer action (BoundBufferTransfer.java; the Bound class of
+    CpuMetalPreparedBufferTransfer.java:222-249): retains the host storage and the device
+    action, allocates nothing when executed."""
+
+    def __init__(self, host: np.ndarray, action):
+        self._host = host
+        self._action = action
+
+    def execute(self) -> None:
+        self._action(self._host)
+
+
+class CpuHipPreparedBufferTransfer:
+    """Immutable CPU<->HIP storage-layout transfer recipe for one prepared logical value
+    (CpuMetalPreparedBufferTransfer.java:16-250, with the HIP integration in Metal's place).
+
+    Construction checks the descriptor's geometry and that the prepared memory slot holds exactly
+    its byte extent; `bind` validates both concrete representations (host storage: C-contiguous,
+    exact byte size, writable when it is the destination; device: HipBackendIntegration's
+    storage-transfer acceptance) and returns the bound action."""
+
+    CPU_TO_HIP = "CPU_TO_HIP"
+    HIP_TO_CPU = "HIP_TO_CPU"
+
+    def __init__(self, hip: HipBackendIntegration, slot_bytes: int,
+                 descriptor: TensorDescriptor, direction: str):
+        if hip is None or descriptor is None or direction is None:
+            raise TypeError("hip, descriptor and direction must not be None")
+        if direction not in (self.CPU_TO_HIP, self.HIP_TO_CPU):
+            raise ValueError(f"unknown CPU/HIP transfer direction {direction}")
+        extent = hip.storage_transfer_extent(descriptor)
+        if extent <= 0:
+            raise ValueError("CPU/HIP transfer requires rank-0..16 static non-overlapping "
+                             "positive-stride storage geometry with a checked byte extent")
+        if int(slot_bytes) != extent:
+            raise ValueError("transfer descriptor byte extent does not match prepared memory slot")
+        self.hip = hip
+        self.descriptor = descriptor
+        self.direction = direction
+        self.byte_count = extent
+
+    @staticmethod
+    def supports(descriptor: TensorDescriptor) -> bool:
+        """CpuMetalPreparedBufferTransfer.supports (CpuMetalPreparedBufferTransfer.java:73-77)."""
+        return storage_transfer_extent(descriptor) > 0
+
+    @classmethod
+    def cpu_to_hip(cls, hip, slot_bytes, descriptor):
+        return cls(hip, slot_bytes, descriptor, cls.CPU_TO_HIP)
+
+    @classmethod
+    def hip_to_cpu(cls, hip, slot_bytes, descriptor):
+        return cls(hip, slot_bytes, descriptor, cls.HIP_TO_CPU)
+
+    def _accepts_host(self, host, writable: bool) -> bool:
+        return (isinstance(host, np.ndarray) and host.flags.c_contiguous
+                and host.nbytes == self.byte_count and (host.flags.writeable or not writable))
+
+    def accepts_source(self, representation) -> bool:
+        if self.direction == self.CPU_TO_HIP:
+            return self._accepts_host(representation, False)
+        return self.hip.accepts_storage_layout_transfer(representation, self.descriptor)
+
+    def accepts_destination(self, representation) -> bool:
+        if self.direction == self.CPU_TO_HIP:
+            return self.hip.accepts_storage_layout_transfer(representation, self.descriptor)
+        return self._accepts_host(representation, True)
+
+    def bind(self, source, destination) -> BoundBufferTransfer:
+        if not self.accepts_source(source) or not self.accepts_destination(destination):
+            raise ValueError("incompatible buffer representation for this CPU/HIP transfer")
+        if self.direction == self.CPU_TO_HIP:
+            return BoundBufferTransfer(
+                source, self.hip.bind_storage_layout_upload(destination, self.descriptor))
+        return BoundBufferTransfer(
+            destination, self.hip.bind_storage_layout_download(source, self.descriptor))
 
 
 # ---------------------------------------------------------------------------------------------

@@ -183,6 +183,11 @@ hipError_t launch_canonical_pack(const void* src, void* dst, int64_t elements, i
                                  int boolean, const CanonicalGeometry* g, uint32_t* status,
                                  hipStream_t s);
 
+// ORs DEV_INVALID_BOOL into *status when any of the `elements` logical BOOL bytes of the view
+// g over src is neither 0 nor 1; reads only.
+hipError_t launch_bool_validate(const void* src, int64_t elements, const CanonicalGeometry& g,
+                                uint32_t* status, hipStream_t s);
+
 // Y[C,R] = X[R,C]^T
 hipError_t launch_transpose(const float* x, float* y, int64_t R, int64_t C, hipStream_t s);
 

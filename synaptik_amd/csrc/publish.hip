@@ -84,8 +84,8 @@ template <> struct Elem<4> { using T = uint32_t; __device__ static T swap(T v) {
 template <> struct Elem<8> { using T = uint64_t; __device__ static T swap(T v) { return __builtin_bswap64(v); } };
 
 // Strided view: ordinal -> storage element by the row-major mixed-radix decomposition of the
-// ordinal over the dimensions (last axis fastest).
-template <int W, bool BOOLV>
+// ordinal over the dimensions (last axis fastest). STORE = false only validates (BOOL).
+template <int W, bool BOOLV, bool STORE = true>
 __global__ void __launch_bounds__(PUB_NT) pack_strided_kernel(const uint8_t* __restrict__ src,
                                                               uint8_t* __restrict__ dst,
                                                               int64_t elements,
@@ -106,7 +106,7 @@ __global__ void __launch_bounds__(PUB_NT) pack_strided_kernel(const uint8_t* __r
     }
     const T v = s[idx];
     if (BOOLV) bad |= v > 1;
-    d[o] = Elem<W>::swap(v);
+    if (STORE) d[o] = Elem<W>::swap(v);
   }
   if (BOOLV) {
     const int any = wave_or(bad ? 1 : 0);
@@ -189,6 +189,15 @@ hipError_t launch_w(const void* src, void* dst, int64_t elements, const Canonica
 }
 
 }  // namespace
+
+hipError_t launch_bool_validate(const void* src, int64_t elements, const CanonicalGeometry& g,
+                                uint32_t* status, hipStream_t s) {
+  if (elements <= 0) return hipSuccess;
+  hipLaunchKernelGGL((pack_strided_kernel<1, true, false>), dim3(grid_for(elements)),
+                     dim3(PUB_NT), 0, s, static_cast<const uint8_t*>(src), nullptr, elements, g,
+                     status);
+  return hipGetLastError();
+}
 
 hipError_t launch_canonical_pack(const void* src, void* dst, int64_t elements, int width,
                                  int boolean, const CanonicalGeometry* g, uint32_t* status,

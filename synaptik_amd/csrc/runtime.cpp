@@ -794,6 +794,216 @@ int32_t shk_hip_buffer_download(void* buffer, uint64_t offset, void* destination
   return SHK_HIP_STATUS_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Grows the context's publication staging buffer (status word in its first 256 bytes, payload
+// after it) to at least `need` bytes. Caller holds the context mutex with the device current.
+int32_t ensure_pub_staging(Context* c, uint64_t need) {
+  if (c->pub_staging_bytes >= need) return SHK_HIP_STATUS_OK;
+  if (c->pub_staging != nullptr) {
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    (void)hipFree(c->pub_staging);
+    c->pub_staging = nullptr;
+    c->pub_staging_bytes = 0;
+  }
+  if (hipMalloc((void**)&c->pub_staging, need) != hipSuccess) {
+    c->pub_staging = nullptr;
+    return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "publication staging of %llu bytes failed",
+                (unsigned long long)need);
+  }
+  c->pub_staging_bytes = need;
+  return SHK_HIP_STATUS_OK;
+}
+
+// Byte extent of a storage-layout transfer, or 0 when the geometry is not one
+// (MetalBackendRuntime.isStorageTransfer / transferByteCount, MetalBackendRuntime.java:433-484;
+// CpuMetalPreparedBufferTransfer.transferByteCount, CpuMetalPreparedBufferTransfer.java:79-127).
+// The axes of extent > 1 are insertion-sorted by stride (a strictly larger stride moves ahead,
+// so equal strides keep axis order); each must start at or beyond the element span the smaller
+// ones cover, which rules out overlap. All arithmetic is checked signed 64-bit, as Java's
+// Math.*Exact is.
+uint64_t storage_transfer_extent(uint32_t width, uint32_t rank, const int64_t* dims,
+                                 const int64_t* strides, int64_t offset) {
+  if (width != 1 && width != 2 && width != 4 && width != 8) return 0;
+  if (rank > (uint32_t)shk::CANONICAL_MAX_RANK || (rank > 0 && dims == nullptr) || offset < 0)
+    return 0;
+  int64_t st[shk::CANONICAL_MAX_RANK];
+  if (strides == nullptr) {  // dense row-major
+    int64_t e = 1;
+    for (int a = (int)rank - 1; a >= 0; --a) {
+      st[a] = e;
+      if (dims[a] > 0 && __builtin_mul_overflow(e, dims[a], &e)) return 0;
+    }
+  } else {
+    for (uint32_t a = 0; a < rank; ++a) st[a] = strides[a];
+  }
+  int64_t as[shk::CANONICAL_MAX_RANK], ad[shk::CANONICAL_MAX_RANK];
+  int active = 0;
+  for (uint32_t a = 0; a < rank; ++a) {
+    if (dims[a] <= 0 || st[a] <= 0) return 0;
+    if (dims[a] > 1) {
+      int i = active;
+      while (i > 0 && as[i - 1] > st[a]) {
+        as[i] = as[i - 1];
+        ad[i] = ad[i - 1];
+        --i;
+      }
+      as[i] = st[a];
+      ad[i] = dims[a];
+      ++active;
+    }
+  }
+  int64_t covered = 1;
+  for (int i = 0; i < active; ++i) {
+    if (as[i] < covered) return 0;
+    int64_t ext;
+    if (__builtin_mul_overflow(ad[i] - 1, as[i], &ext) ||
+        __builtin_add_overflow(covered, ext, &covered))
+      return 0;
+  }
+  int64_t span, bytes;
+  if (__builtin_add_overflow(offset, covered, &span) ||
+      __builtin_mul_overflow(span, (int64_t)width, &bytes) || bytes <= 0)
+    return 0;
+  return (uint64_t)bytes;
+}
+
+// Row-major ordinal walk over a view, calling f(storage element index) for each element.
+template <typename F>
+void for_each_storage_index(uint32_t rank, const int64_t* dims, const int64_t* strides,
+                            int64_t offset, F f) {
+  int64_t st[shk::CANONICAL_MAX_RANK], idx[shk::CANONICAL_MAX_RANK] = {};
+  int64_t e = 1;
+  for (int a = (int)rank - 1; a >= 0; --a) {
+    st[a] = strides != nullptr ? strides[a] : e;
+    e *= dims[a];
+  }
+  int64_t pos = offset;
+  for (;;) {
+    f(pos);
+    int a = (int)rank - 1;
+    for (; a >= 0; --a) {
+      if (++idx[a] < dims[a]) {
+        pos += st[a];
+        break;
+      }
+      pos -= (dims[a] - 1) * st[a];
+      idx[a] = 0;
+    }
+    if (a < 0) return;
+  }
+}
+
+struct StorageTransfer {
+  Buffer* b = nullptr;
+  uint64_t bytes = 0;
+};
+
+// Shared argument checks of the two transfer directions (MetalBackendRuntime.java:211-265).
+int32_t check_storage_transfer(void* buffer, uint32_t& width, int32_t boolean, uint32_t rank,
+                               const int64_t* dims, const int64_t* strides, int64_t offset,
+                               const void* host, uint64_t host_bytes, const char* side,
+                               StorageTransfer* out) {
+  Buffer* b = checked<Buffer, kBufferMagic>(buffer);
+  if (b == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a buffer handle");
+  if (b->ctx->released.load()) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "context is released");
+  if (boolean) width = 1;
+  const uint64_t bytes = storage_transfer_extent(width, rank, dims, strides, offset);
+  if (bytes == 0)
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT,
+                "storage transfer requires rank-0..16 static non-overlapping positive-stride "
+                "geometry with a checked byte extent");
+  if (b->bytes != bytes)
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT,
+                "buffer byte size %llu does not match the transfer extent %llu",
+                (unsigned long long)b->bytes, (unsigned long long)bytes);
+  if (host == nullptr || host_bytes < bytes)
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "%s is smaller than its transfer extent", side);
+  out->b = b;
+  out->bytes = bytes;
+  return SHK_HIP_STATUS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t shk_hip_storage_transfer_bytes(uint32_t element_width, uint32_t rank, const int64_t* dims,
+                                       const int64_t* strides, int64_t storage_offset,
+                                       uint64_t* out_bytes) {
+  if (out_bytes == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "out_bytes is null");
+  *out_bytes = storage_transfer_extent(element_width, rank, dims, strides, storage_offset);
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_buffer_upload_storage(void* buffer, uint32_t element_width, int32_t boolean,
+                                      uint32_t rank, const int64_t* dims, const int64_t* strides,
+                                      int64_t storage_offset, const void* source,
+                                      uint64_t source_bytes) {
+  StorageTransfer t;
+  int32_t st = check_storage_transfer(buffer, element_width, boolean, rank, dims, strides,
+                                      storage_offset, source, source_bytes, "source", &t);
+  if (st != SHK_HIP_STATUS_OK) return st;
+  if (boolean) {  // MetalBackendRuntime.validateBooleanElements before the native write (:241-244)
+    const uint8_t* p = static_cast<const uint8_t*>(source);
+    bool bad = false;
+    for_each_storage_index(rank, dims, strides, storage_offset,
+                           [&](int64_t i) { bad |= p[i] > 1; });
+    if (bad) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "BOOL source contains a non-canonical byte");
+  }
+  Context* c = t.b->ctx;
+  std::lock_guard<std::mutex> lock(c->mutex);
+  HIP_TRY(hipSetDevice(c->device));
+  if (hipMemcpyAsync(t.b->ptr, source, t.bytes, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+      hipStreamSynchronize(c->stream) != hipSuccess)
+    return fail(SHK_HIP_STATUS_COPY_FAILED, "host-to-device copy failed");
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_buffer_download_storage(void* buffer, uint32_t element_width, int32_t boolean,
+                                        uint32_t rank, const int64_t* dims,
+                                        const int64_t* strides, int64_t storage_offset,
+                                        void* destination, uint64_t destination_capacity) {
+  StorageTransfer t;
+  int32_t st = check_storage_transfer(buffer, element_width, boolean, rank, dims, strides,
+                                      storage_offset, destination, destination_capacity,
+                                      "destination", &t);
+  if (st != SHK_HIP_STATUS_OK) return st;
+  Context* c = t.b->ctx;
+  std::lock_guard<std::mutex> lock(c->mutex);
+  HIP_TRY(hipSetDevice(c->device));
+  if (boolean) {
+    // Validation on the device before any byte reaches the destination (the reference downloads
+    // into host staging and validates there, MetalBackendRuntime.java:270-281).
+    st = ensure_pub_staging(c, 256);
+    if (st != SHK_HIP_STATUS_OK) return st;
+    shk::CanonicalGeometry g{};
+    g.rank = (int32_t)rank;
+    g.offset = storage_offset;
+    int64_t elements = 1, e = 1;
+    for (int a = (int)rank - 1; a >= 0; --a) {
+      g.dims[a] = dims[a];
+      g.strides[a] = strides != nullptr ? strides[a] : e;
+      e *= dims[a];
+      elements *= dims[a];
+    }
+    uint32_t* status = reinterpret_cast<uint32_t*>(c->pub_staging);
+    HIP_TRY(shk::launch_fill_u32(status, 1, 0u, c->stream));
+    HIP_TRY(shk::launch_bool_validate(t.b->ptr, elements, g, status, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->host_status, status, 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (*c->host_status & shk::DEV_INVALID_BOOL)
+      return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "BOOL source contains a non-canonical byte");
+  }
+  if (hipMemcpyAsync(destination, t.b->ptr, t.bytes, hipMemcpyDeviceToHost, c->stream) !=
+          hipSuccess ||
+      hipStreamSynchronize(c->stream) != hipSuccess)
+    return fail(SHK_HIP_STATUS_COPY_FAILED, "device-to-host copy failed");
+  return SHK_HIP_STATUS_OK;
+}
+
 int32_t shk_hip_buffer_download_canonical(void* buffer, uint32_t element_width, int32_t boolean,
                                           uint32_t rank, const int64_t* dims,
                                           const int64_t* strides, int64_t storage_offset,
@@ -886,20 +1096,9 @@ int32_t shk_hip_buffer_download_canonical(void* buffer, uint32_t element_width, 
       return fail(SHK_HIP_STATUS_COPY_FAILED, "device-to-host copy failed");
     return SHK_HIP_STATUS_OK;
   }
-  const uint64_t need = 256 + ((byte_count + 255) / 256) * 256;
-  if (c->pub_staging_bytes < need) {
-    if (c->pub_staging != nullptr) {
-      HIP_TRY(hipStreamSynchronize(c->stream));
-      (void)hipFree(c->pub_staging);
-      c->pub_staging = nullptr;
-      c->pub_staging_bytes = 0;
-    }
-    if (hipMalloc((void**)&c->pub_staging, need) != hipSuccess) {
-      c->pub_staging = nullptr;
-      return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "publication staging of %llu bytes failed",
-                  (unsigned long long)need);
-    }
-    c->pub_staging_bytes = need;
+  {
+    const int32_t st = ensure_pub_staging(c, 256 + ((byte_count + 255) / 256) * 256);
+    if (st != SHK_HIP_STATUS_OK) return st;
   }
   uint32_t* status = reinterpret_cast<uint32_t*>(c->pub_staging);
   uint8_t* packed = c->pub_staging + 256;

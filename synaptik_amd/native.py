@@ -54,6 +54,9 @@ EXPORTED_SYMBOLS = (
     "shk_hip_buffer_download",
     "shk_hip_buffer_device_pointer",
     "shk_hip_buffer_download_canonical",
+    "shk_hip_storage_transfer_bytes",
+    "shk_hip_buffer_upload_storage",
+    "shk_hip_buffer_download_storage",
     "shk_hip_program_create",
     "shk_hip_program_release",
     "shk_hip_program_run",
@@ -126,6 +129,17 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
                                                         ctypes.POINTER(ctypes.c_int64),
                                                         ctypes.POINTER(ctypes.c_int64),
                                                         ctypes.c_int64, vp, u64, u64]),
+            "shk_hip_storage_transfer_bytes": (i32, [u32, u32, ctypes.POINTER(ctypes.c_int64),
+                                                     ctypes.POINTER(ctypes.c_int64),
+                                                     ctypes.c_int64, ctypes.POINTER(u64)]),
+            "shk_hip_buffer_upload_storage": (i32, [vp, u32, i32, u32,
+                                                    ctypes.POINTER(ctypes.c_int64),
+                                                    ctypes.POINTER(ctypes.c_int64),
+                                                    ctypes.c_int64, vp, u64]),
+            "shk_hip_buffer_download_storage": (i32, [vp, u32, i32, u32,
+                                                      ctypes.POINTER(ctypes.c_int64),
+                                                      ctypes.POINTER(ctypes.c_int64),
+                                                      ctypes.c_int64, vp, u64]),
             "shk_hip_program_create": (i32, [vp, vp, u64, ctypes.POINTER(vp)]),
             "shk_hip_program_release": (i32, [vp]),
             "shk_hip_program_run": (i32, [vp, u32, ctypes.POINTER(vp), u32, ctypes.POINTER(vp)]),
@@ -210,6 +224,30 @@ class HipContext:
         self.close()
 
 
+def _geometry(shape, strides):
+    shape = tuple(int(d) for d in shape)
+    rank = len(shape)
+    dims = (ctypes.c_int64 * max(1, rank))(*shape)
+    st = None if strides is None else (ctypes.c_int64 * max(1, rank))(*[int(x) for x in strides])
+    return dims, st, rank
+
+
+def storage_transfer_bytes(element_width: int, shape, strides, storage_offset: int) -> int:
+    """Byte extent of a storage-layout transfer of this geometry, 0 when it is not one
+    (`shk_hip_storage_transfer_bytes`, host-only). Extents or offsets outside int64 are not
+    representable and give 0."""
+    lim = 1 << 63
+    vals = [int(d) for d in shape] + [int(x) for x in (strides or ())] + [int(storage_offset)]
+    if any(not -lim <= v < lim for v in vals) or len(tuple(shape)) > 16:
+        return 0
+    lib = load_library()
+    dims, st, rank = _geometry(shape, strides)
+    out = ctypes.c_uint64()
+    check(lib, lib.shk_hip_storage_transfer_bytes(int(element_width), rank, dims, st,
+                                                  int(storage_offset), ctypes.byref(out)))
+    return out.value
+
+
 class HipBuffer:
     """Device buffer handle (`shk_hip_buffer_*`); released exactly once."""
 
@@ -254,6 +292,29 @@ class HipBuffer:
             self.handle, int(element_width), 1 if boolean else 0, rank, dims, st,
             int(storage_offset), out.ctypes.data, nbytes, int(maximum_bytes)))
         return memoryview(out[:nbytes]).toreadonly()
+
+    def upload_storage(self, element_width: int, shape, strides, storage_offset: int,
+                       source, boolean: bool = False) -> None:
+        """Writes the whole physical span of a storage-layout view from host bytes
+        (`shk_hip_buffer_upload_storage`); BOOL logical elements are validated first."""
+        src = np.ascontiguousarray(source).reshape(-1).view(np.uint8)
+        dims, st, rank = _geometry(shape, strides)
+        check(self.lib, self.lib.shk_hip_buffer_upload_storage(
+            self.handle, int(element_width), 1 if boolean else 0, rank, dims, st,
+            int(storage_offset), src.ctypes.data if src.nbytes else None, src.nbytes))
+
+    def download_storage(self, element_width: int, shape, strides, storage_offset: int,
+                         destination: np.ndarray, boolean: bool = False) -> None:
+        """Reads the whole physical span of a storage-layout view into `destination`, a writable
+        C-contiguous host array (`shk_hip_buffer_download_storage`); a BOOL view is validated on
+        the device before any byte is written."""
+        if not (destination.flags.c_contiguous and destination.flags.writeable):
+            raise ValueError("destination must be writable contiguous host storage")
+        dims, st, rank = _geometry(shape, strides)
+        check(self.lib, self.lib.shk_hip_buffer_download_storage(
+            self.handle, int(element_width), 1 if boolean else 0, rank, dims, st,
+            int(storage_offset), destination.ctypes.data if destination.nbytes else None,
+            destination.nbytes))
 
     def device_pointer(self) -> int:
         p = ctypes.c_void_p()

@@ -25,6 +25,7 @@
 // The tile kernel lives in gemm_tile.h and is instantiated per operand layout in gemm_nn.hip,
 // gemm_nt.hip, gemm_tn.hip and gemm_tt.hip; this file holds the dispatch, the deterministic
 // split-K reduction and the K == 1 outer product.
+#include "gemm_skinny.h"
 #include "gemm_tile.h"
 #include "gemm_v2.h"
 #include <algorithm>
@@ -83,7 +84,15 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(GemmParams p, int spli
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
     const int64_t row = e / p.N, col = e - row * p.N;
     float v = p.partial[e];
-    for (int sidx = 1; sidx < splits; ++sidx) v = v + p.partial[sidx * plane + e];
+    int sidx = 1;
+    for (; sidx + 8 <= splits; sidx += 8) {  // eight loads in flight, added in slice order
+      float t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = p.partial[(sidx + u) * plane + e];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v = v + t[u];
+    }
+    for (; sidx < splits; ++sidx) v = v + p.partial[sidx * plane + e];
     if (upd) {
       ok &= update_scalar(p.upd, uc, e, v);
       continue;
@@ -117,7 +126,15 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce4(GemmParams p, int spl
   for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < groups; q += (int64_t)gridDim.x * 256) {
     const int64_t e = 4 * q, row = e / p.N, col = e - row * p.N;
     f4 v = *reinterpret_cast<const f4*>(p.partial + e);
-    for (int sidx = 1; sidx < splits; ++sidx) {
+    int sidx = 1;
+    for (; sidx + 4 <= splits; sidx += 4) {  // four loads in flight, added in slice order
+      f4 t[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) t[u] = *reinterpret_cast<const f4*>(p.partial + (sidx + u) * plane + e);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v = f4{v[0] + t[u][0], v[1] + t[u][1], v[2] + t[u][2], v[3] + t[u][3]};
+    }
+    for (; sidx < splits; ++sidx) {
       const f4 w = *reinterpret_cast<const f4*>(p.partial + sidx * plane + e);
       v = f4{v[0] + w[0], v[1] + w[1], v[2] + w[2], v[3] + w[3]};
     }
@@ -199,6 +216,9 @@ int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K, bool colsum) {
     const int64_t slices = (K + splitk_chunk(K, s) - 1) / splitk_chunk(K, s);
     floats = slices * M * N;
   }
+  floats = std::max<int64_t>(floats, skinny_workspace_floats(M, N, K));
+  if (colsum && K >= 2 && K <= 16)  // small-K kernel: one binary64 partial row per row block
+    floats = std::max<int64_t>(floats, 2 * small_k_row_blocks(M, N) * N);
   if (colsum) {
     // the fused path writes ceil(M/BM) * BM/WM binary64 rows, at most (M + 255) / 32 for every
     // configuration (BM <= 256, WM >= 32); the split path's separate pass needs far fewer
@@ -237,7 +257,14 @@ hipError_t launch_gemm(const GemmParams& in, float* workspace, hipStream_t s) {
   p.colsum_partial = nullptr;
   if (p.colsum == nullptr || p.M <= 0 || p.N <= 0) return launch_gemm_core(p, workspace, s);
   const bool split = use_split(p, workspace != nullptr);
-  if (p.K <= 1 || split) {
+  const SkinnyRoute route = skinny_route(p);
+  if (route == SKINNY_SMALL_K && workspace != nullptr) {  // column sum fused into the kernel
+    p.colsum_partial = reinterpret_cast<double*>(workspace);
+    hipError_t e = launch_gemm_core(p, workspace, s);
+    if (e != hipSuccess) return e;
+    return launch_colsum_finish(p.colsum_partial, p.colsum, g_colsum_rows, p.N, s);
+  }
+  if (p.K <= 1 || split || route != SKINNY_NONE) {
     hipError_t e = launch_gemm_core(p, workspace, s);
     if (e != hipSuccess) return e;
     return launch_colsum(p.C, p.colsum, p.M, p.N, p.ldc, 1.0, 0,
@@ -254,6 +281,9 @@ hipError_t launch_gemm_core(const GemmParams& in, float* workspace, hipStream_t 
   p.partial = nullptr;
   p.kchunk = 0;
   if (p.M <= 0 || p.N <= 0) return hipSuccess;
+  const SkinnyRoute route = skinny_route(p);
+  if (route != SKINNY_NONE && (route != SKINNY_COL_OUTER || workspace != nullptr))
+    return launch_skinny(p, route, workspace, s);
   if (use_split(p, workspace != nullptr)) {
     p.kchunk = splitk_chunk(p.K, splitk_slices(p.M, p.N, p.K));
     const int slices = (int)((p.K + p.kchunk - 1) / p.kchunk);
@@ -262,24 +292,7 @@ hipError_t launch_gemm_core(const GemmParams& in, float* workspace, hipStream_t 
     vector_operands(p, va, vb);
     hipError_t e = launch_tiles(p, va, vb, true, s);
     if (e != hipSuccess) return e;
-    const int64_t total = p.M * p.N;
-    bool vec = p.N % 4 == 0 && aligned16(p.partial);
-    if (p.upd.pn != nullptr) {
-      const GemmUpdate& u = p.upd;
-      vec = vec && aligned16(u.p) && aligned16(u.pn) && (u.m == nullptr || (aligned16(u.m) && aligned16(u.mn))) &&
-            (u.kind == 0 || (aligned16(u.v) && aligned16(u.vn)));
-    } else {
-      vec = vec && aligned16(p.C) && p.ldc % 4 == 0 && (p.bias == nullptr || aligned16(p.bias)) &&
-            (p.mode != 1 || (aligned16(p.aux) && p.ldaux % 4 == 0));
-    }
-    if (vec) {
-      const unsigned blocks = (unsigned)std::min<int64_t>(65536, (total / 4 + 255) / 256);
-      hipLaunchKernelGGL(gemm_splitk_reduce4, dim3(blocks), dim3(256), 0, s, p, slices);
-    } else {
-      const unsigned blocks = (unsigned)std::min<int64_t>(65536, (total + 255) / 256);
-      hipLaunchKernelGGL(gemm_splitk_reduce, dim3(blocks), dim3(256), 0, s, p, slices);
-    }
-    return hipGetLastError();
+    return launch_splitk_finish(p, slices, s);
   }
   if (p.K == 1) {
     const int64_t total = p.M * p.N;
@@ -290,6 +303,27 @@ hipError_t launch_gemm_core(const GemmParams& in, float* workspace, hipStream_t 
   bool va, vb;
   vector_operands(p, va, vb);
   return launch_tiles(p, va, vb, false, s);
+}
+
+hipError_t launch_splitk_finish(const GemmParams& p, int slices, hipStream_t s) {
+  const int64_t total = p.M * p.N;
+  bool vec = p.N % 4 == 0 && aligned16(p.partial);
+  if (p.upd.pn != nullptr) {
+    const GemmUpdate& u = p.upd;
+    vec = vec && aligned16(u.p) && aligned16(u.pn) && (u.m == nullptr || (aligned16(u.m) && aligned16(u.mn))) &&
+          (u.kind == 0 || (aligned16(u.v) && aligned16(u.vn)));
+  } else {
+    vec = vec && aligned16(p.C) && p.ldc % 4 == 0 && (p.bias == nullptr || aligned16(p.bias)) &&
+          (p.mode != 1 || (aligned16(p.aux) && p.ldaux % 4 == 0));
+  }
+  if (vec) {
+    const unsigned blocks = (unsigned)std::min<int64_t>(65536, (total / 4 + 255) / 256);
+    hipLaunchKernelGGL(gemm_splitk_reduce4, dim3(blocks), dim3(256), 0, s, p, slices);
+  } else {
+    const unsigned blocks = (unsigned)std::min<int64_t>(65536, (total + 255) / 256);
+    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(blocks), dim3(256), 0, s, p, slices);
+  }
+  return hipGetLastError();
 }
 
 }  // namespace shk

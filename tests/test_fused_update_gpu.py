@@ -27,7 +27,7 @@ OPTIMIZERS = [
 # tiles, long batch); K == 1 (one row); the large-problem kernel (first layer's 2048x2048
 # weight gradient)
 SHAPES = [([37, 130, 67, 3], 96), ([64, 96, 32, 1], 4096), ([16, 24, 8, 1], 1),
-          ([2048, 2048, 8], 64), ([784, 1024, 8], 1024)]
+          ([2048, 2048, 8], 64), ([784, 1024, 8], 1024), ([784, 1024, 10], 1024)]
 
 
 def _run(ctx, monkeypatch, fuse, spec, Ws, bs, opt, x, y, steps):
@@ -43,7 +43,7 @@ def _bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
-@pytest.mark.parametrize("shape", SHAPES, ids=["tile", "splitk", "k1", "large", "edge64"])
+@pytest.mark.parametrize("shape", SHAPES, ids=["tile", "splitk", "k1", "large", "edge64", "classifier"])
 @pytest.mark.parametrize("opt", OPTIMIZERS, ids=["sgd", "nesterov", "dampening", "adam", "adamw"])
 def test_fused_update_matches_streaming_pass(ctx, monkeypatch, shape, opt):
     widths, batch = shape

@@ -301,3 +301,72 @@ def test_direct_lds_kernel_edges_gradient_column_sum(ctx, shape):
     C = C.reshape(M, N)
     assert np.array_equal(C, oracle.activation_grad("tanh", oracle.matmul(dZ, W), y))
     np.testing.assert_array_max_ulp(db, oracle.colsum(C), maxulp=1)
+
+
+# Skinny problems (one of M, N, K <= 16): the small-K, row-dot and column-outer kernels, with
+# aligned and unaligned extents, every operand layout, long and short contractions.
+SKINNY_SHAPES = [(1, 4096, 4096), (16, 1000, 777), (1000, 16, 513), (3, 5, 100), (17, 16, 2),
+                 (4099, 1027, 2), (1024, 1024, 10), (10, 1024, 1024), (5000, 3, 33),
+                 (2, 2, 70000), (1, 1, 4096), (16, 16, 17), (33, 1028, 16), (1025, 1, 300)]
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("shape", SKINNY_SHAPES, ids=str)
+def test_skinny_integer_operands_bit_exact(ctx, shape, ta, tb):
+    M, N, K = shape
+    rng = np.random.default_rng(M * 7 + N * 13 + K)
+    A = rng.integers(-3, 4, size=(K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.integers(-3, 4, size=(N, K) if tb else (K, N)).astype(np.float32)
+    print(f"skinny M={M} N={N} K={K} ta={ta} tb={tb}", flush=True)
+    C = _gemm_case(ctx, A, B, M, N, K, ta, tb)
+    assert np.array_equal(C, oracle.matmul(A, B, trans_a=ta, trans_b=tb))
+
+
+@pytest.mark.parametrize("ta,tb", [(False, True), (False, False), (True, False), (True, True)])
+@pytest.mark.parametrize("shape", [(1024, 10, 1024), (10, 1024, 1024), (1024, 1024, 10),
+                                   (1, 4096, 4096), (7, 3, 50000)], ids=str)
+def test_skinny_gaussian_within_bound(ctx, shape, ta, tb):
+    M, N, K = shape
+    rng = np.random.default_rng(17)
+    A = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    C = _gemm_case(ctx, A, B, M, N, K, ta, tb)
+    ref = oracle.matmul(A, B, trans_a=ta, trans_b=tb)
+    Ad = np.abs(A.T if ta else A).astype(np.float64)
+    Bd = np.abs(B.T if tb else B).astype(np.float64)
+    u = 2.0 ** -24
+    gamma = K * u / (1 - K * u)
+    assert (np.abs(C.astype(np.float64) - ref) <= 2 * gamma * (Ad @ Bd) + 1e-30).all()
+
+
+@pytest.mark.parametrize("act", ["relu", "tanh", "sigmoid", None])
+@pytest.mark.parametrize("shape", [(1024, 10, 1024), (1, 4096, 512), (300, 16, 12), (5, 37, 3)],
+                         ids=str)
+def test_skinny_bias_activation_epilogue(ctx, act, shape):
+    M, N, K = shape
+    rng = np.random.default_rng(23)
+    X = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    W = rng.integers(-3, 4, size=(N, K)).astype(np.float32) * np.float32(0.125)
+    b = rng.standard_normal(N).astype(np.float32)
+    Y = _gemm_case(ctx, X, W, M, N, K, False, True, bias=b, act=act)
+    assert np.array_equal(Y, oracle.linear_forward(X, W, b, act))
+
+
+@pytest.mark.parametrize("shape", [(1024, 1024, 10), (1000, 1026, 7), (10, 300, 2048), (300, 10, 2048)],
+                         ids=str)
+def test_skinny_activation_gradient_and_column_sum(ctx, shape):
+    M, N, K = shape
+    rng = np.random.default_rng(29)
+    dZ = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    W = rng.integers(-3, 4, size=(K, N)).astype(np.float32)
+    y = oracle.activation("relu", rng.standard_normal((M, N)).astype(np.float32))
+    pb = ProgramBuilder()
+    sa, sb, sy = pb.input(M * K), pb.input(K * N), pb.input(M * N)
+    sc, sd = pb.output(M * N), pb.output(N)
+    pb.gemm(sa, sb, sc, M, N, K, aux=sy, act="relu", act_grad=True, colsum=sd)
+    C, db = run_program(ctx, pb, [dZ, W, y], [sc, sd])
+    ref = oracle.activation_grad("relu", oracle.matmul(dZ, W), y)
+    assert np.array_equal(C.reshape(M, N), ref)
+    np.testing.assert_array_max_ulp(db, oracle.colsum(ref), maxulp=1)
+

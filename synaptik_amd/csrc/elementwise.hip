@@ -237,6 +237,41 @@ __global__ void __launch_bounds__(256) colsum_pass1_v4(const float* __restrict__
   if (gc < N)
     part[(int64_t)blockIdx.y * N + gc] = ((lds[0][c] + lds[1][c]) + lds[2][c]) + lds[3][c];
 }
+// Column sums of a narrow input in one launch (N <= CS_SMALL_MAX_N, R <= CS_SMALL_MAX_R): block
+// x sums 64 columns over all R rows with 16 waves (wave w: rows w, w + 16, ..., eight loads in
+// flight), the waves' binary64 sums are added in wave order through LDS and finished as
+// colsum_pass2 does.
+constexpr int64_t CS_SMALL_MAX_N = 256;
+constexpr int64_t CS_SMALL_MAX_R = 32768;
+__global__ void __launch_bounds__(1024) colsum_small(const float* __restrict__ x, float* out,
+                                                    int64_t R, int64_t N, int64_t ldx,
+                                                    double divisor, int accumulate) {
+  __shared__ double lds[16][CS_COLS];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t col = (int64_t)blockIdx.x * CS_COLS + lane;
+  double s = 0.0;
+  if (col < N) {
+    int64_t r = w;
+    for (; r + 7 * 16 < R; r += 8 * 16) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = x[(r + u * 16) * ldx + col];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += (double)v[u];
+    }
+    for (; r < R; r += 16) s += (double)x[r * ldx + col];
+  }
+  lds[w][lane] = s;
+  __syncthreads();
+  if (w == 0 && col < N) {
+    double t = lds[0][lane];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) t += lds[i][lane];
+    float v = (float)(t / divisor);
+    if (accumulate) v = out[col] + v;
+    out[col] = v;
+  }
+}
 // Column sums, pass 2: block x finishes 64 columns; wave w adds partial rows w, w + 4, ... in
 // two interleaved chains (independent loads in flight), then the chains and the four waves are
 // combined in a fixed order, so results are run-to-run identical.
@@ -400,6 +435,11 @@ int64_t colsum_partial_doubles(int64_t R, int64_t N) {
 hipError_t launch_colsum(const float* x, float* out, int64_t R, int64_t N, int64_t ldx,
                          double divisor, int accumulate, double* partial, hipStream_t s) {
   if (N <= 0) return hipSuccess;
+  if (N <= CS_SMALL_MAX_N && R <= CS_SMALL_MAX_R) {
+    hipLaunchKernelGGL(colsum_small, dim3((unsigned)((N + CS_COLS - 1) / CS_COLS)), dim3(1024), 0,
+                       s, x, out, R, N, ldx, divisor, accumulate);
+    return hipGetLastError();
+  }
   const int64_t rows = colsum_rows_per_panel(R, N);
   const int64_t P = (R + rows - 1) / rows;
   if (P > 0) {

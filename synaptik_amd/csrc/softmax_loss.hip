@@ -421,8 +421,7 @@ __global__ void __launch_bounds__(256) ce_pass1(const float* __restrict__ logits
     part[2 * blockIdx.x + 1] = ((dc[0] + dc[1]) + dc[2]) + dc[3];
   }
 }
-__global__ void __launch_bounds__(256) ce_pass2(double* part, int P, float* loss) {
-  __shared__ double dl[4];
+__device__ __forceinline__ void ce_finish(double* part, int P, float* loss, double* dl) {
   double s = 0.0, c = 0.0;
   for (int i = threadIdx.x; i < P; i += 256) {
     s += part[2 * i];
@@ -436,13 +435,33 @@ __global__ void __launch_bounds__(256) ce_pass2(double* part, int P, float* loss
     part[2 * P] = c;  // non-ignored sample count for the gradient pass
   }
 }
-template <typename T>
+__global__ void __launch_bounds__(256) ce_pass2(double* part, int P, float* loss) {
+  __shared__ double dl[4];
+  ce_finish(part, P, loss, dl);
+}
+// Gradient rows. FUSED: the launch is the one after ce_pass1 (no ce_pass2): block 0 first does
+// ce_pass2's work (same code, same order), and every block sums the P exact per-block sample
+// counts itself (integers in binary64, exact in any order) instead of reading the total.
+template <typename T, bool FUSED>
 __global__ void __launch_bounds__(256) ce_grad(const float* __restrict__ logits,
                                                const T* __restrict__ target, int64_t R, int64_t C,
                                                int has_ignore, int64_t ignore, float g,
-                                               const double* count_ptr,
+                                               double* part, int P, float* loss,
                                                float* __restrict__ grad) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  double count;
+  if (FUSED) {
+    __shared__ double dl[4];
+    if (blockIdx.x == 0) {
+      ce_finish(part, P, loss, dl);
+      __syncthreads();
+    }
+    double c = 0.0;
+    for (int i = threadIdx.x; i < P; i += 256) c += part[2 * i + 1];
+    count = block_sum<256>(c, dl);
+  } else {
+    count = part[2 * P];
+  }
   const int64_t r = (int64_t)blockIdx.x * 4 + w;
   if (r >= R) return;
   const int64_t t = (int64_t)target[r];
@@ -452,7 +471,7 @@ __global__ void __launch_bounds__(256) ce_grad(const float* __restrict__ logits,
     for (int64_t c = lane; c < C; c += 64) gr[c] = 0.0f;
     return;
   }
-  const float scale = g / (float)(*count_ptr);
+  const float scale = g / (float)count;
   const int64_t safe = t < 0 ? 0 : (t >= C ? C - 1 : t);
   float m = -INFINITY;
   for (int64_t c = lane; c < C; c += 64) m = java_max(m, row[c]);
@@ -524,6 +543,7 @@ hipError_t launch_mse(const float* p, const float* t, float* loss, float* grad, 
   return hipGetLastError();
 }
 
+constexpr unsigned CE_FUSE_BLOCKS = 1024;
 int64_t index_ce_partial_doubles(int64_t R) { return 2 * ((R + 3) / 4) + 2; }
 hipError_t launch_index_ce(const float* logits, const void* target, int target_is_64,
                            float* loss, float* grad, int64_t R, int64_t C, int has_ignore,
@@ -537,15 +557,31 @@ hipError_t launch_index_ce(const float* logits, const void* target, int target_i
   else
     hipLaunchKernelGGL(ce_pass1<int32_t>, dim3(blocks), dim3(256), 0, s, logits,
                        (const int32_t*)target, R, C, has_ignore, ignore_index, partial, status);
-  hipLaunchKernelGGL(ce_pass2, dim3(1), dim3(256), 0, s, partial, (int)blocks, loss);
+  const int P = (int)blocks;
+  // Up to CE_FUSE_BLOCKS blocks, the gradient launch also finishes the loss (each block re-sums
+  // the P counts: 2P doubles read per block); beyond that a separate one-block pass does.
+  const bool fuse = grad != nullptr && blocks <= CE_FUSE_BLOCKS;
+  if (!fuse) hipLaunchKernelGGL(ce_pass2, dim3(1), dim3(256), 0, s, partial, P, loss);
   if (grad != nullptr) {
-    const double* count = partial + 2 * blocks;
-    if (target_is_64)
-      hipLaunchKernelGGL(ce_grad<int64_t>, dim3(blocks), dim3(256), 0, s, logits,
-                         (const int64_t*)target, R, C, has_ignore, ignore_index, g, count, grad);
-    else
-      hipLaunchKernelGGL(ce_grad<int32_t>, dim3(blocks), dim3(256), 0, s, logits,
-                         (const int32_t*)target, R, C, has_ignore, ignore_index, g, count, grad);
+    if (target_is_64) {
+      if (fuse)
+        hipLaunchKernelGGL((ce_grad<int64_t, true>), dim3(blocks), dim3(256), 0, s, logits,
+                           (const int64_t*)target, R, C, has_ignore, ignore_index, g, partial, P,
+                           loss, grad);
+      else
+        hipLaunchKernelGGL((ce_grad<int64_t, false>), dim3(blocks), dim3(256), 0, s, logits,
+                           (const int64_t*)target, R, C, has_ignore, ignore_index, g, partial, P,
+                           loss, grad);
+    } else {
+      if (fuse)
+        hipLaunchKernelGGL((ce_grad<int32_t, true>), dim3(blocks), dim3(256), 0, s, logits,
+                           (const int32_t*)target, R, C, has_ignore, ignore_index, g, partial, P,
+                           loss, grad);
+      else
+        hipLaunchKernelGGL((ce_grad<int32_t, false>), dim3(blocks), dim3(256), 0, s, logits,
+                           (const int32_t*)target, R, C, has_ignore, ignore_index, g, partial, P,
+                           loss, grad);
+    }
   }
   return hipGetLastError();
 }

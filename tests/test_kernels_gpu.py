@@ -97,7 +97,7 @@ def test_pointwise_activation_forward_and_grad(ctx, act):
 
 
 # ---- reductions ----
-@pytest.mark.parametrize("R,N", [(1, 1), (4096, 4096), (1000, 10), (8192, 1024), (3, 70000), (517, 12), (1025, 1284)])
+@pytest.mark.parametrize("R,N", [(1, 1), (4096, 4096), (1000, 10), (8192, 1024), (3, 70000), (517, 12), (1025, 1284), (32768, 256), (20000, 100), (32769, 3)])
 def test_colsum_against_exact_oracle(ctx, R, N):
     rng = np.random.default_rng(R + N)
     x = rng.standard_normal((R, N)).astype(np.float32)
@@ -233,7 +233,8 @@ def test_mse_against_oracle(ctx, n, reduction):
 
 @pytest.mark.parametrize("dtype", ["i64", "i32"])
 @pytest.mark.parametrize("ignore", [None, -100])
-@pytest.mark.parametrize("shape", [(1024, 10), (9000, 10), (300, 100)], ids=["c3", "many-rows", "many-classes"])
+@pytest.mark.parametrize("shape", [(1024, 10), (9000, 10), (300, 100), (4096, 10), (4097, 3)],
+                         ids=["c3", "many-rows", "many-classes", "fused-edge", "unfused-edge"])
 def test_index_cross_entropy_against_oracle(ctx, dtype, ignore, shape):
     R, C = shape
     rng = np.random.default_rng(9)
@@ -253,20 +254,23 @@ def test_index_cross_entropy_against_oracle(ctx, dtype, ignore, shape):
                                rtol=1e-5, atol=1e-9)
 
 
+@pytest.mark.parametrize("with_grad", [False, True])
 @pytest.mark.parametrize("shape", [(16, 4), (9000, 4)], ids=["few-rows", "many-rows"])
-def test_index_cross_entropy_out_of_bounds_status(ctx, shape):
+def test_index_cross_entropy_out_of_bounds_status(ctx, shape, with_grad):
     R, C = shape
     pb = ProgramBuilder()
     sx, sy = pb.input(R * C), pb.input(R, "i64")
     sl = pb.output(1)
-    pb.index_ce(sx, sy, sl, R, C)
+    sg = pb.output(R * C) if with_grad else None
+    pb.index_ce(sx, sy, sl, R, C, grad=sg)
+    outs = [sl] + ([sg] if with_grad else [])
     y = np.zeros(R, np.int64)
     y[9] = 4
     with pytest.raises(HipIndexError):
-        run_program(ctx, pb, [np.zeros(R * C, np.float32), y], [sl])
+        run_program(ctx, pb, [np.zeros(R * C, np.float32), y], outs)
     y[9] = -1
     with pytest.raises(HipIndexError):
-        run_program(ctx, pb, [np.zeros(R * C, np.float32), y], [sl])
+        run_program(ctx, pb, [np.zeros(R * C, np.float32), y], outs)
 
 
 # ---- optimizers ----

@@ -60,7 +60,7 @@ struct V2Loader {
   int vrow[Cfg::NI], vk[Cfg::NI];  // first row (M/N) and first k of the chunk in the tile
   uint32_t wdst;                   // this wave's byte offset inside a stage (wave-uniform)
   __device__ __forceinline__ void init(int64_t ld) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = (threadIdx.x >> 6) & 3;
     wdst = __builtin_amdgcn_readfirstlane((uint32_t)w * 1024u);
 #pragma unroll
     for (int i = 0; i < Cfg::NI; ++i) {
@@ -95,7 +95,7 @@ struct V2Loader {
                    : "v"(voff[I]), "s"(tile), "{m0}"(dst)
                    : "memory");
     } else {
-      const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+      const int w = (threadIdx.x >> 6) & 3, lane = threadIdx.x & 63;
       *reinterpret_cast<floatx4*>(lds + (I * 4 + w) * 256 + lane * 4) = floatx4{0.f, 0.f, 0.f, 0.f};
     }
   }
@@ -139,22 +139,33 @@ __device__ __forceinline__ void v2_barrier() {
 }
 
 // The tile kernel. KA: A(m, k) is contiguous along k (A stored [M,K]); KB: B(n, k) is contiguous
-// along k (B stored [N,K]).
-template <bool KA, bool KB, int BT, bool TAIL>
-__global__ void __launch_bounds__(V2_NT) __attribute__((amdgpu_waves_per_eu(2)))
+// along k (B stored [N,K]). KS = 2 splits K inside the workgroup: eight waves in two groups of
+// four, group h runs the whole pipeline below on k-tiles [h T, (h + 1) T), T = ceil(k-tiles / 2),
+// with LDS stages of its own (group 1's last tile is all zeros when the count is odd: TAIL), and
+// group 1 hands its accumulators to group 0 through LDS, which adds them (group 0 + group 1, a
+// fixed order) before the epilogue. It gives each SIMD two waves on problems with too few tiles
+// for two workgroups per CU, without partials in HBM or a second launch.
+template <bool KA, bool KB, int BT, bool TAIL, int KS>
+__global__ void __launch_bounds__(V2_NT * KS) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_f32_v2(GemmParams p) {
   using Cfg = V2Cfg<BT>;
   constexpr int NB = Cfg::NB, WT = Cfg::WT, TILEF = Cfg::TILEF, NI = Cfg::NI, NG = Cfg::NG;
-  __shared__ __attribute__((aligned(16))) float As0[TILEF];
-  __shared__ __attribute__((aligned(16))) float Bs0[TILEF];
-  __shared__ __attribute__((aligned(16))) float As1[TILEF];
-  __shared__ __attribute__((aligned(16))) float Bs1[TILEF];
+  __shared__ __attribute__((aligned(16))) float As0g[KS * TILEF];
+  __shared__ __attribute__((aligned(16))) float Bs0g[KS * TILEF];
+  __shared__ __attribute__((aligned(16))) float As1g[KS * TILEF];
+  __shared__ __attribute__((aligned(16))) float Bs1g[KS * TILEF];
+  // wave-uniform (readfirstlane): tile origins derived from it stay in SGPRs
+  const int kgroup = KS == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8));
+  float* const As0 = As0g + kgroup * TILEF;
+  float* const Bs0 = Bs0g + kgroup * TILEF;
+  float* const As1 = As1g + kgroup * TILEF;
+  float* const Bs1 = Bs1g + kgroup * TILEF;
 
   const int tilesM = (int)((p.M + BT - 1) / BT), tilesN = (int)((p.N + BT - 1) / BT);
   int tm, tn;
   tile_of(blockIdx.x, tilesM, tilesN, tm, tn);
   const int64_t m0 = (int64_t)tm * BT, n0 = (int64_t)tn * BT;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = (threadIdx.x >> 6) & 3;
   const int wm = wave >> 1, wn = wave & 1;
   const int l16 = lane & 15, g = lane >> 4;
   const int rows_a = (int)std::min<int64_t>(BT, p.M - m0);
@@ -162,8 +173,15 @@ gemm_f32_v2(GemmParams p) {
 
   // operand tile origins at k = 0, and the per-k-tile advance
   // split-K: block row y covers k in [y * kchunk, min(K, (y + 1) * kchunk))
-  const int64_t k_begin = p.kchunk > 0 ? (int64_t)blockIdx.y * p.kchunk : 0;
-  const int64_t k_len = p.kchunk > 0 ? std::min<int64_t>(p.kchunk, p.K - k_begin) : p.K;
+  int64_t k_begin = p.kchunk > 0 ? (int64_t)blockIdx.y * p.kchunk : 0;
+  int64_t k_len = p.kchunk > 0 ? std::min<int64_t>(p.kchunk, p.K - k_begin) : p.K;
+  int nk = (int)((k_len + V2_BK - 1) / V2_BK);
+  if constexpr (KS == 2) {  // (no split-K slices with KS = 2)
+    const int half = (nk + 1) / 2;
+    k_begin = (int64_t)kgroup * half * V2_BK;
+    k_len = kgroup == 0 ? std::min<int64_t>(p.K, (int64_t)half * V2_BK) : p.K - k_begin;
+    nk = half;  // group 1: k_len may end inside (or before) its last tile, which TAIL zero-fills
+  }
   const float* a_tile = KA ? p.A + m0 * p.lda + k_begin : p.A + m0 + k_begin * p.lda;
   const float* b_tile = KB ? p.B + n0 * p.ldb + k_begin : p.B + n0 + k_begin * p.ldb;
   const int64_t a_step = KA ? V2_BK : V2_BK * p.lda;
@@ -193,7 +211,6 @@ gemm_f32_v2(GemmParams p) {
     });
   });
 
-  const int nk = (int)((k_len + V2_BK - 1) / V2_BK);
   // 4 NB^2 MFMAs of one half-tile in NG groups of 8 (MFMA n: s = n / NB^2, block
   // i = (n % NB^2) / NB, j = n % NB); after each group, side(q) issues that group's share of the
   // LDS reads and copies. The scheduling barriers keep this order: reads and copies spread over
@@ -338,6 +355,36 @@ gemm_f32_v2(GemmParams p) {
   }
   v2_wait_all();
   v2_barrier();  // every wave has finished reading its fragments: the stages are free
+  if constexpr (KS == 2) {
+    // group 1 -> group 0: accumulator (block I, J, register R) of wave w, lane l at
+    // ((I NB + J) 4 + R) 64 + l of a 4 NB^2 x 64 slab in group 1's (free) stages: waves 0, 1 in
+    // its A0 stage, waves 2, 3 in its B0 stage (two slabs per stage)
+    static_assert(2 * 4 * NB * NB * 64 <= TILEF, "exchange slabs must fit group 1's stages");
+    float* xchg = (wave < 2 ? As0g : Bs0g) + TILEF + (wave & 1) * (4 * NB * NB * 64);
+    if (kgroup == 1) {
+      static_for<NB>([&](auto i) {
+        static_for<NB>([&](auto j) {
+          constexpr int I = decltype(i)::value, J = decltype(j)::value;
+          static_for<4>([&](auto r) {
+            constexpr int R = decltype(r)::value;
+            xchg[((I * NB + J) * 4 + R) * 64 + lane] = acc[I][J][R];
+          });
+        });
+      });
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+    }
+    v2_barrier();
+    if (kgroup == 1) return;
+    static_for<NB>([&](auto i) {
+      static_for<NB>([&](auto j) {
+        constexpr int I = decltype(i)::value, J = decltype(j)::value;
+        static_for<4>([&](auto r) {
+          constexpr int R = decltype(r)::value;
+          acc[I][J][R] = acc[I][J][R] + xchg[((I * NB + J) * 4 + R) * 64 + lane];
+        });
+      });
+    });
+  }
   constexpr int ECPR = Cfg::ECPR, RSTEP = 64 / ECPR, PER_ARRAY = TILEF / (WT * WT);
   const int arr = wave / PER_ARRAY;
   float* stage = (arr == 0 ? As0 : arr == 1 ? Bs0 : arr == 2 ? As1 : Bs1) +
@@ -436,6 +483,15 @@ inline bool v2_enabled() {
   return on;
 }
 
+// In-workgroup split-K is on unless SHK_HIP_GEMM_KS2=0 (read once per process).
+inline bool v2_ks2_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("SHK_HIP_GEMM_KS2");
+    return e == nullptr || atoi(e) != 0;
+  }();
+  return on;
+}
+
 // Kernel choice for a GEMM (0: none, the register-staged kernel runs it; else the tile edge).
 //   * both operands allow 16-byte loads, K and N are multiples of 4 and, for the transposed
 //     epilogue, its pointers are 16-byte aligned with leading dimensions multiples of 4;
@@ -470,17 +526,37 @@ inline int v2_choose(const GemmParams& p, bool va, bool vb) {
   return 0;
 }
 
+// In-workgroup split-K (KS = 2) for 64x64 tiles: fewer than two tiles per CU and at least
+// eight k-tiles per group.
+inline bool v2_split_in_group(const GemmParams& p, int bt) {
+  const int64_t t64 = ((p.M + 63) / 64) * ((p.N + 63) / 64);
+  return v2_ks2_enabled() && bt == 64 && p.kchunk == 0 && t64 < 512 && p.K >= 16 * V2_BK;
+}
+
 template <bool TA, bool TB, int BT>
 hipError_t launch_v2_bt(const GemmParams& p, hipStream_t s) {
   g_colsum_rows = ((p.M + BT - 1) / BT) * 2;
   const unsigned tiles = (unsigned)(((p.M + BT - 1) / BT) * ((p.N + BT - 1) / BT));
   const unsigned slices = p.kchunk > 0 ? (unsigned)((p.K + p.kchunk - 1) / p.kchunk) : 1u;
   const int64_t span = p.kchunk > 0 ? p.kchunk : p.K;
+  if constexpr (BT == 64) {
+    if (v2_split_in_group(p, BT)) {
+      // both groups whole k-tiles only when K is a multiple of 2 BK
+      const bool tail = p.M % BT != 0 || p.N % BT != 0 || p.K % (2 * V2_BK) != 0;
+      if (tail)
+        hipLaunchKernelGGL((gemm_f32_v2<!TA, TB, BT, true, 2>), dim3(tiles), dim3(2 * V2_NT), 0,
+                           s, p);
+      else
+        hipLaunchKernelGGL((gemm_f32_v2<!TA, TB, BT, false, 2>), dim3(tiles), dim3(2 * V2_NT), 0,
+                           s, p);
+      return hipGetLastError();
+    }
+  }
   const bool tail = p.M % BT != 0 || p.N % BT != 0 || span % V2_BK != 0 || p.K % V2_BK != 0;
   if (tail)
-    hipLaunchKernelGGL((gemm_f32_v2<!TA, TB, BT, true>), dim3(tiles, slices), dim3(V2_NT), 0, s, p);
+    hipLaunchKernelGGL((gemm_f32_v2<!TA, TB, BT, true, 1>), dim3(tiles, slices), dim3(V2_NT), 0, s, p);
   else
-    hipLaunchKernelGGL((gemm_f32_v2<!TA, TB, BT, false>), dim3(tiles, slices), dim3(V2_NT), 0, s, p);
+    hipLaunchKernelGGL((gemm_f32_v2<!TA, TB, BT, false, 1>), dim3(tiles, slices), dim3(V2_NT), 0, s, p);
   return hipGetLastError();
 }
 

@@ -370,3 +370,52 @@ def test_skinny_activation_gradient_and_column_sum(ctx, shape):
     assert np.array_equal(C.reshape(M, N), ref)
     np.testing.assert_array_max_ulp(db, oracle.colsum(ref), maxulp=1)
 
+
+
+# In-workgroup split-K (64x64 tiles, fewer than 512 of them, K >= 512): two groups of four waves
+# on the two halves of the k-tiles, an odd count zero-filling group 1's last tile.
+KS2_SHAPES = [(1024, 1024, 512), (1024, 1024, 544), (960, 1000, 1000), (512, 512, 2048),
+              (1000, 1028, 777), (640, 1024, 4096)]
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("shape", KS2_SHAPES, ids=str)
+def test_split_in_group_integer_bit_exact(ctx, shape, ta, tb):
+    M, N, K = shape
+    rng = np.random.default_rng(M + 3 * N + 7 * K)
+    A = rng.integers(-3, 4, size=(K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.integers(-3, 4, size=(N, K) if tb else (K, N)).astype(np.float32)
+    print(f"ks2 M={M} N={N} K={K} ta={ta} tb={tb}", flush=True)
+    C = _gemm_case(ctx, A, B, M, N, K, ta, tb)
+    assert np.array_equal(C, oracle.matmul(A, B, trans_a=ta, trans_b=tb))
+
+
+@pytest.mark.parametrize("shape", [(1024, 1024, 1024), (1000, 1028, 777)], ids=str)
+def test_split_in_group_gradient_column_sum(ctx, shape):
+    M, N, K = shape
+    rng = np.random.default_rng(41)
+    dZ = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    W = rng.integers(-3, 4, size=(K, N)).astype(np.float32)
+    y = oracle.activation("relu", rng.standard_normal((M, N)).astype(np.float32))
+    pb = ProgramBuilder()
+    sa, sb, sy = pb.input(M * K), pb.input(K * N), pb.input(M * N)
+    sc, sd = pb.output(M * N), pb.output(N)
+    pb.gemm(sa, sb, sc, M, N, K, aux=sy, act="relu", act_grad=True, colsum=sd)
+    C, db = run_program(ctx, pb, [dZ, W, y], [sc, sd])
+    ref = oracle.activation_grad("relu", oracle.matmul(dZ, W), y)
+    assert np.array_equal(C.reshape(M, N), ref)
+    np.testing.assert_array_max_ulp(db, oracle.colsum(ref), maxulp=1)
+
+
+def test_split_in_group_gaussian_within_bound(ctx):
+    M, N, K = 1024, 784, 1024
+    rng = np.random.default_rng(43)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K)).astype(np.float32)
+    C = _gemm_case(ctx, A, B, M, N, K, False, True)
+    ref = oracle.matmul(A, B, trans_b=True)
+    u = 2.0 ** -24
+    gamma = K * u / (1 - K * u)
+    bound = 2 * gamma * (np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64).T) + 1e-30
+    assert (np.abs(C.astype(np.float64) - ref) <= bound).all()

@@ -46,6 +46,66 @@ __device__ __noinline__ float pw_exp(float a) { return (float)exp((double)a); }
 __device__ __noinline__ float pw_log(float a) { return (float)log((double)a); }
 __device__ __noinline__ float pw_sqrt(float a) { return (float)sqrt((double)a); }
 
+// One instruction's value from its operands (a, b, c registers; imm for CONST). Shared by the
+// interpreter (op known at run time) and the single-op kernels (op a template constant).
+__device__ __forceinline__ float pw_op(int op, float a, float b, float c, float imm) {
+  switch (op) {
+    case PW_CONST: return imm;
+    case PW_ADD: return a + b;
+    case PW_SUB: return a - b;
+    case PW_MUL: return a * b;
+    case PW_DIV: return a / b;
+    case PW_NEG: return -a;
+    case PW_RELU: return relu_f(a);
+    case PW_TANH: return pw_tanh(a);
+    case PW_SIGMOID: return pw_sigmoid(a);
+    case PW_EXP: return pw_exp(a);
+    case PW_LOG: return pw_log(a);
+    case PW_RELU_GRAD: return act_grad(ACT_RELU, b, a);
+    case PW_TANH_GRAD: return act_grad(ACT_TANH, b, a);
+    case PW_SIGMOID_GRAD: return act_grad(ACT_SIGMOID, b, a);
+    case PW_GT: return a > b ? 1.0f : 0.0f;
+    case PW_WHERE: return (c != 0.0f) ? a : b;
+    case PW_STORE: return a;
+    case PW_MAX: return java_max(a, b);
+    case PW_SQRT: return pw_sqrt(a);
+    default: return 0.0f;
+  }
+}
+
+// Single-op chains (LOAD x [, LOAD y], OP, STORE) over full-shape, 16-byte aligned operands (out
+// may be one of them: each element is read before it is written): out
+// = OP(x, y) element by element with the interpreter's arithmetic (pw_op), streaming 16-byte
+// accesses, two groups of four per thread and iteration, no interpreter.
+template <int OP, bool BIN>
+__global__ void __launch_bounds__(256) pw_single_kernel(const float* x,
+                                                        const float* y,
+                                                        float* out, int64_t n) {
+  const int64_t n4 = n / 4;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < n4; q += 2 * stride) {
+    const bool two = q + stride < n4;
+    const float4 xa = ld_stream(reinterpret_cast<const float4*>(x) + q);
+    const float4 ya = BIN ? ld_stream(reinterpret_cast<const float4*>(y) + q) : xa;
+    float4 xb = xa, yb = ya;
+    if (two) {
+      xb = ld_stream(reinterpret_cast<const float4*>(x) + q + stride);
+      yb = BIN ? ld_stream(reinterpret_cast<const float4*>(y) + q + stride) : xb;
+    }
+    st_stream(reinterpret_cast<float4*>(out) + q,
+              make_float4(pw_op(OP, xa.x, ya.x, 0.f, 0.f), pw_op(OP, xa.y, ya.y, 0.f, 0.f),
+                          pw_op(OP, xa.z, ya.z, 0.f, 0.f), pw_op(OP, xa.w, ya.w, 0.f, 0.f)));
+    if (two)
+      st_stream(reinterpret_cast<float4*>(out) + q + stride,
+                make_float4(pw_op(OP, xb.x, yb.x, 0.f, 0.f), pw_op(OP, xb.y, yb.y, 0.f, 0.f),
+                            pw_op(OP, xb.z, yb.z, 0.f, 0.f), pw_op(OP, xb.w, yb.w, 0.f, 0.f)));
+  }
+  if (blockIdx.x == 0 && threadIdx.x < n - n4 * 4) {
+    const int64_t i = n4 * 4 + threadIdx.x;
+    out[i] = pw_op(OP, x[i], BIN ? y[i] : x[i], 0.f, 0.f);
+  }
+}
+
 // Loads input k for the 4-element group starting at e0 (cnt valid elements) into v.
 __device__ __forceinline__ void pw_load4(const PwParams& p, int k, int64_t e0, int cnt, float (&v)[4]) {
   const float* src = p.in[k];
@@ -105,30 +165,7 @@ __device__ __forceinline__ void pw_exec(const PwParams& p, PwRegs& R, int64_t e0
     }
     float d[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      switch (ins.op) {
-        case PW_CONST: d[q] = ins.imm; break;
-        case PW_ADD: d[q] = a[q] + b[q]; break;
-        case PW_SUB: d[q] = a[q] - b[q]; break;
-        case PW_MUL: d[q] = a[q] * b[q]; break;
-        case PW_DIV: d[q] = a[q] / b[q]; break;
-        case PW_NEG: d[q] = -a[q]; break;
-        case PW_RELU: d[q] = relu_f(a[q]); break;
-        case PW_TANH: d[q] = pw_tanh(a[q]); break;
-        case PW_SIGMOID: d[q] = pw_sigmoid(a[q]); break;
-        case PW_EXP: d[q] = pw_exp(a[q]); break;
-        case PW_LOG: d[q] = pw_log(a[q]); break;
-        case PW_RELU_GRAD: d[q] = act_grad(ACT_RELU, b[q], a[q]); break;
-        case PW_TANH_GRAD: d[q] = act_grad(ACT_TANH, b[q], a[q]); break;
-        case PW_SIGMOID_GRAD: d[q] = act_grad(ACT_SIGMOID, b[q], a[q]); break;
-        case PW_GT: d[q] = a[q] > b[q] ? 1.0f : 0.0f; break;
-        case PW_WHERE: d[q] = (c[q] != 0.0f) ? a[q] : b[q]; break;
-        case PW_STORE: d[q] = a[q]; break;
-        case PW_MAX: d[q] = java_max(a[q], b[q]); break;
-        case PW_SQRT: d[q] = pw_sqrt(a[q]); break;
-        default: d[q] = 0.0f; break;
-      }
-    }
+    for (int q = 0; q < 4; ++q) d[q] = pw_op(ins.op, a[q], b[q], c[q], ins.imm);
     if (ins.op == PW_STORE) {
       float* o = outv[ins.dst & 1];
       o[0] = d[0]; o[1] = d[1]; o[2] = d[2]; o[3] = d[3];
@@ -398,10 +435,84 @@ unsigned grid_for(int64_t n, int per_thread, int nt = 256) {
 
 }  // namespace
 
+namespace {
+// Recognizes a single-op chain: LOAD x -> rx [, LOAD y -> ry], OP (operands among rx, ry) -> rd,
+// STORE rd -> out[o], every operand full-shape and 16-byte aligned. Fills the operand order the
+// op reads (a, b) and returns the op, or -1.
+int pw_single_op(const PwParams& p, const float** a, const float** b, float** out, bool* binary) {
+  auto aligned = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
+  const int n = p.n_instr;
+  if (n != 3 && n != 4) return -1;
+  const int nl = n - 2;
+  int reg[2];
+  const float* src[2];
+  for (int i = 0; i < nl; ++i) {
+    const PwInstr& l = p.code[i];
+    if (l.op != PW_LOAD) return -1;
+    const int k = l.a % PW_MAX_INPUTS;
+    if (p.in[k] == nullptr || p.in_mode[k] != 0 || !aligned(p.in[k])) return -1;
+    reg[i] = l.dst & (PW_REGS - 1);
+    src[i] = p.in[k];
+  }
+  if (nl == 2 && reg[0] == reg[1]) return -1;
+  const PwInstr& op = p.code[nl];
+  const PwInstr& st = p.code[nl + 1];
+  if (st.op != PW_STORE || (st.a & (PW_REGS - 1)) != (op.dst & (PW_REGS - 1))) return -1;
+  float* o = p.out[st.dst & 1];
+  if (o == nullptr || !aligned(o)) return -1;
+  auto which = [&](int r) -> const float* {
+    for (int i = 0; i < nl; ++i)
+      if (reg[i] == (r & (PW_REGS - 1))) return src[i];
+    return nullptr;
+  };
+  const bool bin = op.op == PW_ADD || op.op == PW_SUB || op.op == PW_MUL || op.op == PW_DIV ||
+                   op.op == PW_MAX || op.op == PW_GT || op.op == PW_RELU_GRAD ||
+                   op.op == PW_TANH_GRAD || op.op == PW_SIGMOID_GRAD;
+  const bool un = op.op == PW_NEG || op.op == PW_RELU || op.op == PW_TANH ||
+                  op.op == PW_SIGMOID || op.op == PW_EXP || op.op == PW_LOG || op.op == PW_SQRT;
+  if (!bin && !un) return -1;
+  *a = which(op.a);
+  *b = bin ? which(op.b) : *a;
+  if (*a == nullptr || *b == nullptr) return -1;
+  *out = o;
+  *binary = bin;
+  return op.op;
+}
+
+template <int OP>
+void launch_single(const float* a, const float* b, float* out, int64_t n, bool bin, hipStream_t s) {
+  const unsigned g = grid_for(n, 8);
+  if (bin) hipLaunchKernelGGL((pw_single_kernel<OP, true>), dim3(g), dim3(256), 0, s, a, b, out, n);
+  else hipLaunchKernelGGL((pw_single_kernel<OP, false>), dim3(g), dim3(256), 0, s, a, b, out, n);
+}
+}  // namespace
+
 hipError_t launch_pointwise(const PwParams& p, hipStream_t s) {
   const int64_t n = p.R * p.C;
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(pointwise_kernel, dim3(grid_for(n, 4)), dim3(PW_NT), 0, s, p);
+  const float *a, *b;
+  float* out;
+  bool bin;
+  switch (pw_single_op(p, &a, &b, &out, &bin)) {
+    case PW_ADD: launch_single<PW_ADD>(a, b, out, n, bin, s); break;
+    case PW_SUB: launch_single<PW_SUB>(a, b, out, n, bin, s); break;
+    case PW_MUL: launch_single<PW_MUL>(a, b, out, n, bin, s); break;
+    case PW_DIV: launch_single<PW_DIV>(a, b, out, n, bin, s); break;
+    case PW_MAX: launch_single<PW_MAX>(a, b, out, n, bin, s); break;
+    case PW_GT: launch_single<PW_GT>(a, b, out, n, bin, s); break;
+    case PW_RELU_GRAD: launch_single<PW_RELU_GRAD>(a, b, out, n, bin, s); break;
+    case PW_TANH_GRAD: launch_single<PW_TANH_GRAD>(a, b, out, n, bin, s); break;
+    case PW_SIGMOID_GRAD: launch_single<PW_SIGMOID_GRAD>(a, b, out, n, bin, s); break;
+    case PW_NEG: launch_single<PW_NEG>(a, b, out, n, bin, s); break;
+    case PW_RELU: launch_single<PW_RELU>(a, b, out, n, bin, s); break;
+    case PW_TANH: launch_single<PW_TANH>(a, b, out, n, bin, s); break;
+    case PW_SIGMOID: launch_single<PW_SIGMOID>(a, b, out, n, bin, s); break;
+    case PW_EXP: launch_single<PW_EXP>(a, b, out, n, bin, s); break;
+    case PW_LOG: launch_single<PW_LOG>(a, b, out, n, bin, s); break;
+    case PW_SQRT: launch_single<PW_SQRT>(a, b, out, n, bin, s); break;
+    default:
+      hipLaunchKernelGGL(pointwise_kernel, dim3(grid_for(n, 4)), dim3(PW_NT), 0, s, p);
+  }
   return hipGetLastError();
 }
 

@@ -440,3 +440,36 @@ def test_softmax_special_rows(ctx, C, log):
         np.testing.assert_allclose(g_row[fin], w_row[fin], rtol=2e-6, atol=2e-6 if log else 1e-30)
         zero = fin & (w_row == 0)
         assert np.array_equal(np.signbit(g_row[zero]), np.signbit(w_row[zero]))
+
+
+# ---- single-op pointwise kernels ----
+SINGLE_OPS = ["add", "sub", "mul", "div", "max", "gt", "relu_grad", "tanh_grad", "sigmoid_grad",
+              "neg", "relu", "tanh", "sigmoid", "exp", "log", "sqrt"]
+UNARY = {"neg", "relu", "tanh", "sigmoid", "exp", "log", "sqrt"}
+
+
+@pytest.mark.parametrize("n", [3, 4, 10007, 3 * 8 * 256 * 4 + 5])
+@pytest.mark.parametrize("op", SINGLE_OPS)
+def test_single_op_kernel_matches_interpreter(ctx, op, n):
+    """A LOAD [LOAD] OP STORE chain runs on the dedicated single-op kernel; the same chain with
+    one extra (unused) CONST instruction runs on the interpreter. Both must agree bit for bit,
+    special values included."""
+    rng = np.random.default_rng(n)
+    special = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1e-40, -1e-40, 3e38, 1.0, -1.0],
+                       np.float32)
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    y = (rng.standard_normal(n) * 3).astype(np.float32)
+    x[: min(n, 10)] = special[: min(n, 10)]
+    y[: min(n, 10)] = special[::-1][: min(n, 10)]
+    outs = []
+    for extra in (False, True):
+        pb = ProgramBuilder()
+        sx, sy, so = pb.input(n), pb.input(n), pb.output(n)
+        code = [("load", 0, 0, 0, 0, 0.0), ("load", 1, 1, 0, 0, 0.0)]
+        if extra:
+            code.append(("const", 5, 0, 0, 0, 2.0))
+        code += [(op, 2, 0, 0 if op in UNARY else 1, 0, 0.0), ("store", 0, 2, 0, 0, 0.0)]
+        pb.pointwise(1, n, [sx, sy], [so], code)
+        (o,) = run_program(ctx, pb, [x, y], [so])
+        outs.append(o.view(np.uint32))
+    assert np.array_equal(outs[0], outs[1])

@@ -375,7 +375,8 @@ def test_skinny_activation_gradient_and_column_sum(ctx, shape):
 # In-workgroup split-K (64x64 tiles, fewer than 512 of them, K >= 512): two groups of four waves
 # on the two halves of the k-tiles, an odd count zero-filling group 1's last tile.
 KS2_SHAPES = [(1024, 1024, 512), (1024, 1024, 544), (960, 1000, 1000), (512, 512, 2048),
-              (1000, 1028, 777), (640, 1024, 4096)]
+              (1000, 1028, 777), (640, 1024, 4096), (1024, 1024, 1024), (1024, 1024, 1056),
+              (960, 1000, 2000), (1000, 1028, 1540)]
 
 
 @pytest.mark.parametrize("ta", [False, True])
@@ -391,7 +392,8 @@ def test_split_in_group_integer_bit_exact(ctx, shape, ta, tb):
     assert np.array_equal(C, oracle.matmul(A, B, trans_a=ta, trans_b=tb))
 
 
-@pytest.mark.parametrize("shape", [(1024, 1024, 1024), (1000, 1028, 777)], ids=str)
+@pytest.mark.parametrize("shape", [(1024, 1024, 1024), (1000, 1028, 777), (1000, 1028, 1540)],
+                         ids=str)
 def test_split_in_group_gradient_column_sum(ctx, shape):
     M, N, K = shape
     rng = np.random.default_rng(41)

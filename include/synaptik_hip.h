@@ -80,6 +80,16 @@ int32_t shk_hip_buffer_release(void* buffer);
 int32_t shk_hip_buffer_upload(void* buffer, uint64_t offset, const void* source, uint64_t byte_count);
 int32_t shk_hip_buffer_download(void* buffer, uint64_t offset, void* destination, uint64_t byte_count);
 int32_t shk_hip_buffer_device_pointer(void* buffer, void** out_pointer);
+/* Staged upload of caller host memory (pageable or not): the bytes are copied through a ring of
+ * context-owned pinned chunks and moved by DMA on a second stream of the context, so the copy
+ * overlaps device work. Returns once the source has been read in full (it may be reused) and the
+ * last DMA is enqueued. Ordering: every later use of the buffer through this library (a run, a
+ * download, an upload, a transfer) waits for the DMA; the DMA waits for the last asynchronous
+ * run that bound the buffer. Replaces the pageable upload behind the reference's per-run borrow
+ * of host tensors (MetalBackendRuntime.borrow, MetalBackendRuntime.java:173-200) when batches
+ * stream in from the host; a HIP addition for pinned staging. */
+int32_t shk_hip_buffer_upload_staged(void* buffer, uint64_t offset, const void* source,
+                                     uint64_t byte_count);
 /* Canonical host publication. Replaces the host-side packing of
  * MetalBackendRuntime.copyToCanonicalHostBytes (modules/backend/metal/src/main/java/io/github/
  * pho001/synaptik/backend/metal/MetalBackendRuntime.java:304-424, HostTensorValue.java:18):
@@ -144,6 +154,15 @@ int32_t shk_hip_program_release(void* program);
  * Concurrent runs of one program serialize on its arena. */
 int32_t shk_hip_program_run(void* program, uint32_t input_count, void* const* inputs,
                             uint32_t output_count, void* const* outputs);
+/* shk_hip_program_run without the wait: binds, validates and enqueues the run, then returns;
+ * shk_hip_program_wait completes it and maps its status word exactly as shk_hip_program_run
+ * would. A run, set_profiling, set_graph_mode or step_times call on a program whose
+ * asynchronous run is pending first waits for it, and returns that run's failure if it failed.
+ * HIP addition (the reference's BoundInvocation.executeBound is synchronous): it lets a host
+ * batch upload (shk_hip_buffer_upload_staged) overlap the previous run. */
+int32_t shk_hip_program_run_async(void* program, uint32_t input_count, void* const* inputs,
+                                  uint32_t output_count, void* const* outputs);
+int32_t shk_hip_program_wait(void* program);
 /* Arena bytes owned by the program (internal slots + scratch). */
 int32_t shk_hip_program_arena_bytes(void* program, uint64_t* out_bytes);
 /* Per-step device timing with HIP events on the context stream. Enabling clears the totals. */

@@ -65,6 +65,13 @@ struct Context {
   // Grown on demand, guarded by `mutex`, freed with the context.
   uint8_t* pub_staging = nullptr;
   uint64_t pub_staging_bytes = 0;
+  // Staged uploads (shk_hip_buffer_upload_staged): a second stream at the default priority and a
+  // ring of pinned host chunks, created on first use, freed with the context.
+  hipStream_t copy_stream = nullptr;
+  uint8_t* ring[4] = {nullptr, nullptr, nullptr, nullptr};
+  hipEvent_t ring_free[4] = {nullptr, nullptr, nullptr, nullptr};
+  bool ring_used[4] = {false, false, false, false};
+  int ring_next = 0;
   std::mutex mutex;
   std::atomic<int64_t> refs{1};
   std::atomic<bool> released{false};
@@ -73,6 +80,14 @@ struct Context {
 void context_unref(Context* c) {
   if (c->refs.fetch_sub(1) != 1) return;
   (void)hipSetDevice(c->device);
+  if (c->copy_stream != nullptr) {
+    (void)hipStreamSynchronize(c->copy_stream);
+    (void)hipStreamDestroy(c->copy_stream);
+  }
+  for (int i = 0; i < 4; ++i) {
+    if (c->ring_free[i] != nullptr) (void)hipEventDestroy(c->ring_free[i]);
+    if (c->ring[i] != nullptr) (void)hipHostFree(c->ring[i]);
+  }
   (void)hipStreamSynchronize(c->stream);
   (void)hipStreamDestroy(c->stream);
   (void)hipHostFree(c->host_status);
@@ -87,7 +102,23 @@ struct Buffer {
   void* ptr = nullptr;
   uint64_t bytes = 0;
   bool owned = true;
+  // Cross-stream ordering (guarded by ctx->mutex): a staged upload into this buffer still in
+  // flight on the copy stream (upload_done), and the end of the last asynchronous run that bound
+  // it on the compute stream (last_use). Created on first use.
+  hipEvent_t upload_done = nullptr;
+  bool upload_pending = false;
+  hipEvent_t last_use = nullptr;
+  bool use_pending = false;
 };
+
+// Orders `stream` after a staged upload into b that may still be in flight (caller holds the
+// context mutex).
+hipError_t order_after_upload(Buffer* b, hipStream_t stream) {
+  if (!b->upload_pending) return hipSuccess;
+  const hipError_t e = hipStreamWaitEvent(stream, b->upload_done, 0);
+  if (e == hipSuccess && stream == b->ctx->stream) b->upload_pending = false;
+  return e;
+}
 
 enum SlotKind : uint32_t { SLOT_INTERNAL = 0, SLOT_INPUT = 1, SLOT_OUTPUT = 2, SLOT_INOUT = 3 };
 enum DType : uint32_t { DT_F32 = 0, DT_I32 = 1, DT_I64 = 2, DT_U8 = 3, DT_F64 = 4 };
@@ -160,6 +191,11 @@ struct Program {
   uint64_t profiled_runs = 0;
   std::vector<double> step_ms;
   std::vector<hipEvent_t> events;
+  // Asynchronous runs (shk_hip_program_run_async): the run's status word lands in host_status
+  // (pinned, this program's own) and `done` marks its end; `pending` until waited for.
+  uint32_t* host_status = nullptr;
+  hipEvent_t done = nullptr;
+  bool pending = false;
 };
 
 template <typename T, uint32_t M>
@@ -625,10 +661,14 @@ hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipSt
   }
 }
 
+int32_t finish_run_locked(Program* pr);
+
 void destroy_program(Program* p) {
   if (p == nullptr) return;
   for (auto& kv : p->graph_cache) (void)hipGraphExecDestroy(kv.second);
   for (hipEvent_t e : p->events) (void)hipEventDestroy(e);
+  if (p->done != nullptr) (void)hipEventDestroy(p->done);
+  if (p->host_status != nullptr) (void)hipHostFree(p->host_status);
   if (p->arena != nullptr) (void)hipFree(p->arena);
   p->magic = 0;
   Context* c = p->ctx;
@@ -751,10 +791,12 @@ int32_t shk_hip_buffer_wrap(void* context, void* device_pointer, uint64_t byte_s
 int32_t shk_hip_buffer_release(void* buffer) {
   Buffer* b = checked<Buffer, kBufferMagic>(buffer);
   if (b == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a buffer handle");
-  if (b->owned && b->ptr != nullptr) {
-    (void)hipSetDevice(b->ctx->device);
-    (void)hipFree(b->ptr);
-  }
+  (void)hipSetDevice(b->ctx->device);
+  if (b->upload_pending) (void)hipEventSynchronize(b->upload_done);
+  if (b->use_pending) (void)hipEventSynchronize(b->last_use);
+  if (b->upload_done != nullptr) (void)hipEventDestroy(b->upload_done);
+  if (b->last_use != nullptr) (void)hipEventDestroy(b->last_use);
+  if (b->owned && b->ptr != nullptr) (void)hipFree(b->ptr);
   b->magic = 0;
   Context* c = b->ctx;
   delete b;
@@ -771,6 +813,7 @@ int32_t shk_hip_buffer_upload(void* buffer, uint64_t offset, const void* source,
   if (byte_count == 0) return SHK_HIP_STATUS_OK;
   std::lock_guard<std::mutex> lock(b->ctx->mutex);
   HIP_TRY(hipSetDevice(b->ctx->device));
+  HIP_TRY(order_after_upload(b, b->ctx->stream));
   if (hipMemcpyAsync(static_cast<char*>(b->ptr) + offset, source, byte_count, hipMemcpyHostToDevice,
                      b->ctx->stream) != hipSuccess ||
       hipStreamSynchronize(b->ctx->stream) != hipSuccess)
@@ -787,6 +830,7 @@ int32_t shk_hip_buffer_download(void* buffer, uint64_t offset, void* destination
   if (byte_count == 0) return SHK_HIP_STATUS_OK;
   std::lock_guard<std::mutex> lock(b->ctx->mutex);
   HIP_TRY(hipSetDevice(b->ctx->device));
+  HIP_TRY(order_after_upload(b, b->ctx->stream));
   if (hipMemcpyAsync(destination, static_cast<const char*>(b->ptr) + offset, byte_count,
                      hipMemcpyDeviceToHost, b->ctx->stream) != hipSuccess ||
       hipStreamSynchronize(b->ctx->stream) != hipSuccess)
@@ -814,6 +858,32 @@ int32_t ensure_pub_staging(Context* c, uint64_t need) {
                 (unsigned long long)need);
   }
   c->pub_staging_bytes = need;
+  return SHK_HIP_STATUS_OK;
+}
+
+constexpr uint64_t kRingChunk = 8ull << 20;  // bytes per pinned staging chunk
+constexpr int kRingSlots = 4;
+
+// Creates the copy stream (default priority) and the pinned staging ring on first use (caller
+// holds the context mutex with the device current).
+int32_t ensure_copy_ring(Context* c) {
+  if (c->copy_stream == nullptr &&
+      hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking) != hipSuccess) {
+    c->copy_stream = nullptr;
+    return fail(SHK_HIP_STATUS_NO_COMMAND_QUEUE, "copy stream creation failed");
+  }
+  for (int i = 0; i < kRingSlots; ++i) {  // (resumes where an earlier failed attempt stopped)
+    if (c->ring[i] == nullptr &&
+        hipHostMalloc((void**)&c->ring[i], kRingChunk, hipHostMallocDefault) != hipSuccess) {
+      c->ring[i] = nullptr;
+      return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "pinned staging chunk allocation failed");
+    }
+    if (c->ring_free[i] == nullptr &&
+        hipEventCreateWithFlags(&c->ring_free[i], hipEventDisableTiming) != hipSuccess) {
+      c->ring_free[i] = nullptr;
+      return fail(SHK_HIP_STATUS_DEVICE_ERROR, "event creation failed");
+    }
+  }
   return SHK_HIP_STATUS_OK;
 }
 
@@ -930,6 +1000,47 @@ int32_t check_storage_transfer(void* buffer, uint32_t& width, int32_t boolean, u
 
 extern "C" {
 
+int32_t shk_hip_buffer_upload_staged(void* buffer, uint64_t offset, const void* source,
+                                     uint64_t byte_count) {
+  Buffer* b = checked<Buffer, kBufferMagic>(buffer);
+  if (b == nullptr || (source == nullptr && byte_count != 0))
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid upload arguments");
+  if (b->ctx->released.load()) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "context is released");
+  if (offset > b->bytes || byte_count > b->bytes - offset)
+    return fail(SHK_HIP_STATUS_RANGE_OUT_OF_BOUNDS, "upload range outside the buffer");
+  if (byte_count == 0) return SHK_HIP_STATUS_OK;
+  Context* c = b->ctx;
+  std::lock_guard<std::mutex> lock(c->mutex);
+  HIP_TRY(hipSetDevice(c->device));
+  {
+    const int32_t st = ensure_copy_ring(c);
+    if (st != SHK_HIP_STATUS_OK) return st;
+  }
+  if (b->upload_done == nullptr)
+    HIP_TRY(hipEventCreateWithFlags(&b->upload_done, hipEventDisableTiming));
+  // not before the last asynchronous run that bound this buffer has finished with it
+  if (b->use_pending) HIP_TRY(hipStreamWaitEvent(c->copy_stream, b->last_use, 0));
+  const uint8_t* src = static_cast<const uint8_t*>(source);
+  uint8_t* dst = static_cast<uint8_t*>(b->ptr) + offset;
+  for (uint64_t done = 0; done < byte_count;) {
+    const uint64_t n = std::min<uint64_t>(kRingChunk, byte_count - done);
+    const int slot = c->ring_next;
+    c->ring_next = (c->ring_next + 1) % kRingSlots;
+    if (c->ring_used[slot] && hipEventSynchronize(c->ring_free[slot]) != hipSuccess)
+      return fail(SHK_HIP_STATUS_COPY_FAILED, "host-to-device copy failed");
+    memcpy(c->ring[slot], src + done, n);
+    if (hipMemcpyAsync(dst + done, c->ring[slot], n, hipMemcpyHostToDevice, c->copy_stream) !=
+            hipSuccess ||
+        hipEventRecord(c->ring_free[slot], c->copy_stream) != hipSuccess)
+      return fail(SHK_HIP_STATUS_COPY_FAILED, "host-to-device copy failed");
+    c->ring_used[slot] = true;
+    done += n;
+  }
+  HIP_TRY(hipEventRecord(b->upload_done, c->copy_stream));
+  b->upload_pending = true;
+  return SHK_HIP_STATUS_OK;
+}
+
 int32_t shk_hip_storage_transfer_bytes(uint32_t element_width, uint32_t rank, const int64_t* dims,
                                        const int64_t* strides, int64_t storage_offset,
                                        uint64_t* out_bytes) {
@@ -956,6 +1067,7 @@ int32_t shk_hip_buffer_upload_storage(void* buffer, uint32_t element_width, int3
   Context* c = t.b->ctx;
   std::lock_guard<std::mutex> lock(c->mutex);
   HIP_TRY(hipSetDevice(c->device));
+  HIP_TRY(order_after_upload(t.b, c->stream));
   if (hipMemcpyAsync(t.b->ptr, source, t.bytes, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
       hipStreamSynchronize(c->stream) != hipSuccess)
     return fail(SHK_HIP_STATUS_COPY_FAILED, "host-to-device copy failed");
@@ -974,6 +1086,7 @@ int32_t shk_hip_buffer_download_storage(void* buffer, uint32_t element_width, in
   Context* c = t.b->ctx;
   std::lock_guard<std::mutex> lock(c->mutex);
   HIP_TRY(hipSetDevice(c->device));
+  HIP_TRY(order_after_upload(t.b, c->stream));
   if (boolean) {
     // Validation on the device before any byte reaches the destination (the reference downloads
     // into host staging and validates there, MetalBackendRuntime.java:270-281).
@@ -1088,6 +1201,7 @@ int32_t shk_hip_buffer_download_canonical(void* buffer, uint32_t element_width, 
   Context* c = b->ctx;
   std::lock_guard<std::mutex> lock(c->mutex);
   HIP_TRY(hipSetDevice(c->device));
+  HIP_TRY(order_after_upload(b, c->stream));
   // raw little-endian single bytes need no device pass
   if (dense && element_width == 1 && !boolean) {
     if (hipMemcpyAsync(destination, b->ptr, byte_count, hipMemcpyDeviceToHost, c->stream) !=
@@ -1231,6 +1345,16 @@ int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_
       destroy_program(pr);
       return fail(SHK_HIP_STATUS_DEVICE_ERROR, "arena initialisation failed");
     }
+    if (hipHostMalloc((void**)&pr->host_status, 16, hipHostMallocDefault) != hipSuccess) {
+      pr->host_status = nullptr;
+      destroy_program(pr);
+      return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "pinned status allocation failed");
+    }
+    if (hipEventCreateWithFlags(&pr->done, hipEventDisableTiming) != hipSuccess) {
+      pr->done = nullptr;
+      destroy_program(pr);
+      return fail(SHK_HIP_STATUS_DEVICE_ERROR, "event creation failed");
+    }
     pr->status = static_cast<uint32_t*>(pr->arena);
     pr->scratch = reinterpret_cast<double*>(static_cast<char*>(pr->arena) + scratch_off);
     pr->step_ms.assign(h.n_steps, 0.0);
@@ -1272,6 +1396,10 @@ int32_t shk_hip_program_set_graph_mode(void* program, int32_t enabled) {
   Program* pr = checked<Program, kProgramMagic>(program);
   if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
   std::lock_guard<std::mutex> lock(pr->run_mutex);
+  if (pr->pending) {  // a pending asynchronous run completes (and reports) first
+    const int32_t st = finish_run_locked(pr);
+    if (st != SHK_HIP_STATUS_OK) return st;
+  }
   pr->graphs = enabled != 0;
   return SHK_HIP_STATUS_OK;
 }
@@ -1287,6 +1415,10 @@ int32_t shk_hip_program_set_profiling(void* program, int32_t enabled) {
   Program* pr = checked<Program, kProgramMagic>(program);
   if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
   std::lock_guard<std::mutex> lock(pr->run_mutex);
+  if (pr->pending) {  // a pending asynchronous run completes (and reports) first
+    const int32_t st = finish_run_locked(pr);
+    if (st != SHK_HIP_STATUS_OK) return st;
+  }
   if (enabled && pr->events.empty()) {
     (void)hipSetDevice(pr->ctx->device);
     pr->events.resize(pr->steps.size() + 1, nullptr);
@@ -1303,13 +1435,49 @@ int32_t shk_hip_program_step_times(void* program, double* out_milliseconds, uint
   if (pr == nullptr || (out_milliseconds == nullptr && capacity != 0))
     return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid arguments");
   std::lock_guard<std::mutex> lock(pr->run_mutex);
+  if (pr->pending) {  // a pending asynchronous run completes (and reports) first
+    const int32_t st = finish_run_locked(pr);
+    if (st != SHK_HIP_STATUS_OK) return st;
+  }
   for (uint32_t i = 0; i < capacity && i < pr->step_ms.size(); ++i) out_milliseconds[i] = pr->step_ms[i];
   if (out_runs) *out_runs = pr->profiled_runs;
   return SHK_HIP_STATUS_OK;
 }
 
-int32_t shk_hip_program_run(void* program, uint32_t input_count, void* const* inputs,
-                            uint32_t output_count, void* const* outputs) {
+}  // extern "C"
+
+namespace {
+
+// Waits for the program's pending run and maps its status word (caller holds run_mutex).
+int32_t finish_run_locked(Program* pr) {
+  if (!pr->pending) return SHK_HIP_STATUS_OK;
+  const hipError_t se = hipEventSynchronize(pr->done);
+  pr->pending = false;
+  if (se != hipSuccess)
+    return fail(SHK_HIP_STATUS_EXECUTION_FAILED, "program execution failed: %s", hipGetErrorName(se));
+  if (pr->profiling) {
+    for (size_t i = 0; i < pr->steps.size(); ++i) {
+      float ms = 0.f;
+      HIP_TRY(hipEventElapsedTime(&ms, pr->events[i], pr->events[i + 1]));
+      pr->step_ms[i] += ms;
+    }
+    pr->profiled_runs++;
+  }
+  const uint32_t st = *pr->host_status;
+  if (st & shk::DEV_INDEX_OUT_OF_BOUNDS)
+    return fail(SHK_HIP_STATUS_INDEX_OUT_OF_BOUNDS, "index target out of bounds");
+  if (st & shk::DEV_NOT_POSITIVE)
+    return fail(SHK_HIP_STATUS_ARITHMETIC, "adaptive bias correction or denominator is not positive");
+  if (st & shk::DEV_NON_FINITE)
+    return fail(SHK_HIP_STATUS_ARITHMETIC, "optimizer intermediate or candidate is not finite");
+  return SHK_HIP_STATUS_OK;
+}
+
+// Binds, validates and enqueues one run on the context stream; synchronous runs then wait for it,
+// asynchronous ones return with it pending. A run of a program whose previous asynchronous run
+// is still pending first waits for that one and returns its failure, if any, without launching.
+int32_t run_program(void* program, uint32_t input_count, void* const* inputs, uint32_t output_count,
+                    void* const* outputs, bool async) {
   Program* pr = checked<Program, kProgramMagic>(program);
   if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
   if (input_count != pr->n_inputs || output_count != pr->n_outputs)
@@ -1358,9 +1526,16 @@ int32_t shk_hip_program_run(void* program, uint32_t input_count, void* const* in
     }
 
     std::lock_guard<std::mutex> run_lock(pr->run_mutex);
-    std::lock_guard<std::mutex> ctx_lock(pr->ctx->mutex);
+    if (pr->pending) {
+      const int32_t st = finish_run_locked(pr);
+      if (st != SHK_HIP_STATUS_OK) return st;
+    }
+    std::unique_lock<std::mutex> ctx_lock(pr->ctx->mutex);
     HIP_TRY(hipSetDevice(pr->ctx->device));
     hipStream_t stream = pr->ctx->stream;
+    std::vector<Buffer*> bound(in);
+    bound.insert(bound.end(), out.begin(), out.end());
+    for (Buffer* x : bound) HIP_TRY(order_after_upload(x, stream));  // staged uploads landed
     bool launched = false;
     if (pr->graphs && !pr->profiling) {
       auto it = pr->graph_cache.find(b.ptr);
@@ -1413,31 +1588,46 @@ int32_t shk_hip_program_run(void* program, uint32_t input_count, void* const* in
       }
       if (pr->profiling) HIP_TRY(hipEventRecord(pr->events[pr->steps.size()], stream));
     }
-    HIP_TRY(hipMemcpyAsync(pr->ctx->host_status, pr->status, 4, hipMemcpyDeviceToHost, stream));
-    const hipError_t se = hipStreamSynchronize(stream);
-    if (se != hipSuccess)
-      return fail(SHK_HIP_STATUS_EXECUTION_FAILED, "program execution failed: %s", hipGetErrorName(se));
-    if (pr->profiling) {
-      for (size_t i = 0; i < pr->steps.size(); ++i) {
-        float ms = 0.f;
-        HIP_TRY(hipEventElapsedTime(&ms, pr->events[i], pr->events[i + 1]));
-        pr->step_ms[i] += ms;
+    HIP_TRY(hipMemcpyAsync(pr->host_status, pr->status, 4, hipMemcpyDeviceToHost, stream));
+    HIP_TRY(hipEventRecord(pr->done, stream));
+    pr->pending = true;
+    if (async) {
+      // a later staged upload into any bound buffer waits for this run (write-after-read)
+      for (Buffer* x : bound) {
+        if (x->last_use == nullptr) HIP_TRY(hipEventCreateWithFlags(&x->last_use, hipEventDisableTiming));
+        HIP_TRY(hipEventRecord(x->last_use, stream));
+        x->use_pending = true;
       }
-      pr->profiled_runs++;
+      return SHK_HIP_STATUS_OK;
     }
-    const uint32_t st = *pr->ctx->host_status;
-    if (st & shk::DEV_INDEX_OUT_OF_BOUNDS)
-      return fail(SHK_HIP_STATUS_INDEX_OUT_OF_BOUNDS, "index target out of bounds");
-    if (st & shk::DEV_NOT_POSITIVE)
-      return fail(SHK_HIP_STATUS_ARITHMETIC, "adaptive bias correction or denominator is not positive");
-    if (st & shk::DEV_NON_FINITE)
-      return fail(SHK_HIP_STATUS_ARITHMETIC, "optimizer intermediate or candidate is not finite");
-    return SHK_HIP_STATUS_OK;
+    ctx_lock.unlock();
+    return finish_run_locked(pr);
   } catch (const std::bad_alloc&) {
     return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "host allocation failed");
   } catch (...) {
     return fail(SHK_HIP_STATUS_INTERNAL_ERROR, "unexpected exception");
   }
 }
+}  // namespace
+
+extern "C" {
+
+int32_t shk_hip_program_run(void* program, uint32_t input_count, void* const* inputs,
+                            uint32_t output_count, void* const* outputs) {
+  return run_program(program, input_count, inputs, output_count, outputs, false);
+}
+
+int32_t shk_hip_program_run_async(void* program, uint32_t input_count, void* const* inputs,
+                                  uint32_t output_count, void* const* outputs) {
+  return run_program(program, input_count, inputs, output_count, outputs, true);
+}
+
+int32_t shk_hip_program_wait(void* program) {
+  Program* pr = checked<Program, kProgramMagic>(program);
+  if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
+  std::lock_guard<std::mutex> run_lock(pr->run_mutex);
+  return finish_run_locked(pr);
+}
+
 
 }  // extern "C"

@@ -53,6 +53,7 @@ EXPORTED_SYMBOLS = (
     "shk_hip_buffer_upload",
     "shk_hip_buffer_download",
     "shk_hip_buffer_device_pointer",
+    "shk_hip_buffer_upload_staged",
     "shk_hip_buffer_download_canonical",
     "shk_hip_storage_transfer_bytes",
     "shk_hip_buffer_upload_storage",
@@ -60,6 +61,8 @@ EXPORTED_SYMBOLS = (
     "shk_hip_program_create",
     "shk_hip_program_release",
     "shk_hip_program_run",
+    "shk_hip_program_run_async",
+    "shk_hip_program_wait",
     "shk_hip_program_arena_bytes",
     "shk_hip_program_set_profiling",
     "shk_hip_program_step_times",
@@ -125,6 +128,7 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
             "shk_hip_buffer_upload": (i32, [vp, u64, vp, u64]),
             "shk_hip_buffer_download": (i32, [vp, u64, vp, u64]),
             "shk_hip_buffer_device_pointer": (i32, [vp, ctypes.POINTER(vp)]),
+            "shk_hip_buffer_upload_staged": (i32, [vp, u64, vp, u64]),
             "shk_hip_buffer_download_canonical": (i32, [vp, u32, i32, u32,
                                                         ctypes.POINTER(ctypes.c_int64),
                                                         ctypes.POINTER(ctypes.c_int64),
@@ -143,6 +147,8 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
             "shk_hip_program_create": (i32, [vp, vp, u64, ctypes.POINTER(vp)]),
             "shk_hip_program_release": (i32, [vp]),
             "shk_hip_program_run": (i32, [vp, u32, ctypes.POINTER(vp), u32, ctypes.POINTER(vp)]),
+            "shk_hip_program_run_async": (i32, [vp, u32, ctypes.POINTER(vp), u32, ctypes.POINTER(vp)]),
+            "shk_hip_program_wait": (i32, [vp]),
             "shk_hip_program_arena_bytes": (i32, [vp, ctypes.POINTER(u64)]),
             "shk_hip_program_set_profiling": (i32, [vp, i32]),
             "shk_hip_program_step_times": (i32, [vp, ctypes.POINTER(ctypes.c_double), u32,
@@ -267,6 +273,13 @@ class HipBuffer:
         a = np.ascontiguousarray(array)
         check(self.lib, self.lib.shk_hip_buffer_upload(self.handle, offset, a.ctypes.data, a.nbytes))
 
+    def upload_staged(self, array: np.ndarray, offset: int = 0) -> None:
+        """Upload through the context's pinned staging ring on its copy stream
+        (`shk_hip_buffer_upload_staged`): returns once `array` has been read; the DMA may still be
+        in flight and every later use of this buffer waits for it."""
+        a = np.ascontiguousarray(array)
+        check(self.lib, self.lib.shk_hip_buffer_upload_staged(self.handle, offset, a.ctypes.data, a.nbytes))
+
     def download(self, dtype=np.float32, count: int | None = None, offset: int = 0) -> np.ndarray:
         dt = np.dtype(dtype)
         n = (self.nbytes - offset) // dt.itemsize if count is None else count
@@ -348,6 +361,16 @@ class HipProgram:
         ins = (ctypes.c_void_p * max(1, len(inputs)))(*[b.handle.value for b in inputs])
         outs = (ctypes.c_void_p * max(1, len(outputs)))(*[b.handle.value for b in outputs])
         check(self.lib, self.lib.shk_hip_program_run(self.handle, len(inputs), ins, len(outputs), outs))
+
+    def run_async(self, inputs, outputs) -> None:
+        """Enqueues one run and returns (`shk_hip_program_run_async`); `wait` completes it."""
+        ins = (ctypes.c_void_p * max(1, len(inputs)))(*[b.handle.value for b in inputs])
+        outs = (ctypes.c_void_p * max(1, len(outputs)))(*[b.handle.value for b in outputs])
+        check(self.lib, self.lib.shk_hip_program_run_async(self.handle, len(inputs), ins, len(outputs), outs))
+
+    def wait(self) -> None:
+        """Completes the pending asynchronous run, raising its failure (`shk_hip_program_wait`)."""
+        check(self.lib, self.lib.shk_hip_program_wait(self.handle))
 
     def arena_bytes(self) -> int:
         v = ctypes.c_uint64()

@@ -399,6 +399,7 @@ class HipTrainingSession:
         self.loss = ctx.buffer(4)
         self._x = ctx.buffer(lay.x.nbytes)
         self._y = ctx.buffer(lay.y.nbytes)
+        self._x2 = self._y2 = None  # second batch buffers of run_pipelined, made on first use
 
     @classmethod
     def open(cls, ctx, spec, weights, biases, optimizer, batch, **kw) -> "HipTrainingSession":
@@ -469,6 +470,45 @@ class HipTrainingSession:
         self.run_resident(self._x, self._y, mode)
         step = None if mode == GradientMode.ACCUMULATE else self.optimizer_steps
         return TrainingStep(float(self.objective()), step, self.accumulated_gradient_runs)
+
+    def run_pipelined(self, batches, mode: str = GradientMode.RESET_AND_STEP) -> list:
+        """One run per (x, y) host batch of `batches`, each step's batch uploaded through the
+        context's pinned staging ring on its copy stream while the previous step runs
+        (`shk_hip_buffer_upload_staged`, `shk_hip_program_run_async`), into two alternating
+        batch buffers. Results, state and failure behaviour are those of calling `run` once per
+        batch: a failed step raises, commits nothing, and no later step runs. RESET_AND_STEP
+        without pending accumulated gradients is pipelined; other cases run step by step."""
+        if mode != GradientMode.RESET_AND_STEP or self.accumulated_gradient_runs > 0:
+            return [self.run(x, y, mode) for x, y in batches]
+        if self._x2 is None:
+            self._x2 = self.ctx.buffer(self._x.nbytes)
+            self._y2 = self.ctx.buffer(self._y.nbytes)
+        xs, ys = (self._x, self._x2), (self._y, self._y2)
+        ydt = np.float32 if self.spec.loss == "mse" else (
+            np.int64 if self.label_dtype == "i64" else np.int32)
+        it = iter(batches)
+        nxt = next(it, None)
+        if nxt is None:
+            return []
+        slot = 0
+        xs[slot].upload_staged(np.ascontiguousarray(nxt[0], np.float32))
+        ys[slot].upload_staged(np.ascontiguousarray(nxt[1], ydt))
+        prog, _ = self._programs[(mode, False)]
+        steps = []
+        while nxt is not None:
+            cur = self._sets[self._cur]
+            cand = self._sets[1 - self._cur]
+            prog.run_async(cur[0] + cur[1] + cur[2] + cur[3] + cand[0] + cand[1] + cand[2] + cand[3]
+                           + [self.counter, xs[slot], ys[slot]], [self.loss])
+            nxt = next(it, None)
+            if nxt is not None:  # overlaps the run just enqueued
+                xs[1 - slot].upload_staged(np.ascontiguousarray(nxt[0], np.float32))
+                ys[1 - slot].upload_staged(np.ascontiguousarray(nxt[1], ydt))
+            prog.wait()  # raises (and commits nothing) if the step failed
+            self._cur = 1 - self._cur
+            steps.append(TrainingStep(float(self.objective()), self.optimizer_steps, 0))
+            slot = 1 - slot
+        return steps
 
     def zero_grad(self) -> None:
         """Empties the pending gradient accumulator (TrainingSession.zeroGrad)."""

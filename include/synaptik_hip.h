@@ -163,6 +163,15 @@ int32_t shk_hip_program_run(void* program, uint32_t input_count, void* const* in
 int32_t shk_hip_program_run_async(void* program, uint32_t input_count, void* const* inputs,
                                   uint32_t output_count, void* const* outputs);
 int32_t shk_hip_program_wait(void* program);
+/* Two-stream step schedule (HIP addition; on by default unless SHK_HIP_CONCURRENT=0 when the
+ * program is created): at creation each step's slot reads and writes give its dependencies, and a
+ * step that does not depend on the step at the tail of the context stream runs beside it on a
+ * second stream of the context (its own reduction scratch), joined back by events -- e.g. the
+ * input- and weight-gradient GEMMs of one layer. Results are those of the one-stream order.
+ * set_concurrent(0) runs every step on the context stream, (1) restores the plan;
+ * side_steps reports how many steps the active plan puts on the second stream. */
+int32_t shk_hip_program_set_concurrent(void* program, int32_t enabled);
+int32_t shk_hip_program_side_steps(void* program, uint32_t* out_steps);
 /* Arena bytes owned by the program (internal slots + scratch). */
 int32_t shk_hip_program_arena_bytes(void* program, uint64_t* out_bytes);
 /* Per-step device timing with HIP events on the context stream. Enabling clears the totals. */

@@ -68,6 +68,9 @@ struct Context {
   // Staged uploads (shk_hip_buffer_upload_staged): a second stream at the default priority and a
   // ring of pinned host chunks, created on first use, freed with the context.
   hipStream_t copy_stream = nullptr;
+  // Second compute stream (default priority) for the steps a program schedules beside the main
+  // chain; created with the first program that uses it.
+  hipStream_t side_stream = nullptr;
   uint8_t* ring[4] = {nullptr, nullptr, nullptr, nullptr};
   hipEvent_t ring_free[4] = {nullptr, nullptr, nullptr, nullptr};
   bool ring_used[4] = {false, false, false, false};
@@ -87,6 +90,10 @@ void context_unref(Context* c) {
   for (int i = 0; i < 4; ++i) {
     if (c->ring_free[i] != nullptr) (void)hipEventDestroy(c->ring_free[i]);
     if (c->ring[i] != nullptr) (void)hipHostFree(c->ring[i]);
+  }
+  if (c->side_stream != nullptr) {
+    (void)hipStreamSynchronize(c->side_stream);
+    (void)hipStreamDestroy(c->side_stream);
   }
   (void)hipStreamSynchronize(c->stream);
   (void)hipStreamDestroy(c->stream);
@@ -196,6 +203,17 @@ struct Program {
   uint32_t* host_status = nullptr;
   hipEvent_t done = nullptr;
   bool pending = false;
+  // Two-stream schedule (plan_streams): step j runs on the context stream (0) or its side
+  // stream (1, with scratch_side as its reduction scratch), first waiting for the events
+  // recorded after the steps in wait_for[j]; record_after[j] marks steps other-stream steps
+  // depend on. `concurrent` is false when every step stays on stream 0.
+  bool concurrent = false;
+  uint32_t side_steps = 0;  // steps the plan puts on stream 1 (0: single-stream plan)
+  double* scratch_side = nullptr;
+  std::vector<uint8_t> stream_of, record_after;
+  std::vector<std::vector<uint32_t>> wait_for;
+  std::vector<hipEvent_t> step_done;
+  hipEvent_t fork = nullptr, join = nullptr;
 };
 
 template <typename T, uint32_t M>
@@ -557,7 +575,8 @@ struct Bound {
   T* get(int32_t s) const { return s < 0 ? nullptr : static_cast<T*>(ptr[s]); }
 };
 
-hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipStream_t stream) {
+hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipStream_t stream,
+                        double* scratch) {
   const StepRecord& r = st.rec;
   const int32_t* s = r.slot;
   const int64_t* a = r.iarg;
@@ -589,16 +608,16 @@ hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipSt
         u.completed_steps = b.get<const int64_t>(s[6]);
         u.status = pr.status;
       }
-      return shk::launch_gemm(p, reinterpret_cast<float*>(pr.scratch), stream);
+      return shk::launch_gemm(p, reinterpret_cast<float*>(scratch), stream);
     }
     case OP_COLSUM:
       return shk::launch_colsum(b.get<const float>(s[0]), b.get<float>(s[1]), a[0], a[1], a[2],
-                                a[4] ? (double)a[0] : 1.0, (int)a[3], pr.scratch, stream);
+                                a[4] ? (double)a[0] : 1.0, (int)a[3], scratch, stream);
     case OP_ROW_REDUCE:
       return shk::launch_row_reduce(b.get<const float>(s[0]), b.get<float>(s[1]), a[0], a[1], (int)a[2], stream);
     case OP_REDUCE_ALL:
       return shk::launch_reduce_all(b.get<const float>(s[0]), b.get<float>(s[1]), a[0], (int)a[1],
-                                    pr.scratch, stream);
+                                    scratch, stream);
     case OP_POINTWISE: {
       shk::PwParams p{};
       for (int k = 0; k < shk::PW_MAX_INPUTS; ++k) {
@@ -622,11 +641,11 @@ hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipSt
                                  r.farg[0], b.get<float>(s[3]), a[0], a[1], stream);
     case OP_MSE:
       return shk::launch_mse(b.get<const float>(s[0]), b.get<const float>(s[1]), b.get<float>(s[2]),
-                             b.get<float>(s[3]), a[0], r.farg[0], (int)a[1], pr.scratch, stream);
+                             b.get<float>(s[3]), a[0], r.farg[0], (int)a[1], scratch, stream);
     case OP_CE_INDEX:
       return shk::launch_index_ce(b.get<const float>(s[0]), b.get<const void>(s[1]), (int)a[2],
                                   b.get<float>(s[2]), b.get<float>(s[3]), a[0], a[1], (int)a[3], a[4],
-                                  r.farg[0], pr.scratch, pr.status, stream);
+                                  r.farg[0], scratch, pr.status, stream);
     case OP_OPTIMIZER: {
       shk::OptParams p{};
       const OptEntry* e = reinterpret_cast<const OptEntry*>(st.payload.data());
@@ -661,6 +680,145 @@ hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipSt
   }
 }
 
+// Slots a step reads and writes (and whether it reads the status word, which the other steps
+// only OR bits into). Reduction scratch is not a slot: each stream has its own.
+struct Access {
+  std::vector<int32_t> r, w;
+  bool status_read = false, status_or = false;
+};
+Access step_access(const Step& st) {
+  const StepRecord& rec = st.rec;
+  const int32_t* sl = rec.slot;
+  const int64_t* a = rec.iarg;
+  Access x;
+  auto R = [&](int32_t v) { if (v >= 0) x.r.push_back(v); };
+  auto W = [&](int32_t v) { if (v >= 0) x.w.push_back(v); };
+  switch (rec.opcode) {
+    case OP_GEMM:
+      R(sl[0]); R(sl[1]); R(sl[3]); R(sl[4]); W(sl[2]); W(sl[5]);
+      if (a[11]) R(sl[2]);  // accumulate
+      if (!st.payload.empty()) {
+        const OptEntry& e = *reinterpret_cast<const OptEntry*>(st.payload.data());
+        R(e.p); R(e.m); R(e.v); W(e.pn); W(e.mn); W(e.vn); R(sl[6]);
+        x.status_or = true;
+      }
+      break;
+    case OP_COLSUM: R(sl[0]); W(sl[1]); if (a[3]) R(sl[1]); break;
+    case OP_ROW_REDUCE: case OP_REDUCE_ALL: case OP_COPY: case OP_TRANSPOSE:
+      R(sl[0]); W(sl[1]); break;
+    case OP_POINTWISE:
+      for (int k = 0; k < shk::PW_MAX_INPUTS; ++k) R(sl[k]);
+      W(sl[6]); W(sl[7]);
+      break;
+    case OP_SOFTMAX: R(sl[0]); W(sl[1]); W(sl[2]); break;
+    case OP_SOFTMAX_BWD: R(sl[0]); R(sl[1]); R(sl[3]); W(sl[2]); break;
+    case OP_LSE_BWD: R(sl[0]); R(sl[1]); R(sl[2]); W(sl[3]); break;
+    case OP_MSE: R(sl[0]); R(sl[1]); W(sl[2]); W(sl[3]); break;
+    case OP_CE_INDEX: R(sl[0]); R(sl[1]); W(sl[2]); W(sl[3]); x.status_or = true; break;
+    case OP_OPTIMIZER: {
+      const OptEntry* e = reinterpret_cast<const OptEntry*>(st.payload.data());
+      const size_t n = st.payload.size() / sizeof(OptEntry);
+      for (size_t i = 0; i < n; ++i) {
+        R(e[i].g); R(e[i].p); W(e[i].p); R(e[i].m); W(e[i].m); R(e[i].v); W(e[i].v);
+        W(e[i].pn); W(e[i].mn); W(e[i].vn);
+      }
+      R(sl[0]);
+      x.status_or = true;
+      break;
+    }
+    case OP_STEP_COMMIT: R(sl[0]); W(sl[0]); x.status_read = true; break;
+    case OP_FILL: W(sl[0]); break;
+    default:  // unknown: conflicts with everything
+      x.status_read = true;
+      W(-2);
+  }
+  return x;
+}
+bool accesses_conflict(const Access& a, const Access& b) {
+  auto meet = [](const std::vector<int32_t>& u, const std::vector<int32_t>& v) {
+    for (int32_t p : u)
+      for (int32_t q : v)
+        if (p == q || p == -2 || q == -2) return true;
+    return false;
+  };
+  return meet(a.w, b.r) || meet(a.w, b.w) || meet(a.r, b.w) ||
+         (a.status_read && (b.status_or || b.status_read)) || (b.status_read && a.status_or);
+}
+bool concurrency_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("SHK_HIP_CONCURRENT");
+    return !(e != nullptr && e[0] == '0');
+  }();
+  return on;
+}
+// Two-stream list schedule: step j goes beside the main chain (stream 1) when it does not
+// depend on the step currently at the tail of stream 0; a step waits (event) for every earlier
+// step on the other stream it depends on. Steps on one stream keep program order.
+void plan_streams(Program* pr) {
+  const size_t n = pr->steps.size();
+  pr->stream_of.assign(n, 0);
+  pr->record_after.assign(n, 0);
+  pr->wait_for.assign(n, {});
+  pr->concurrent = false;
+  if (!concurrency_enabled() || n < 2) return;
+  std::vector<Access> acc(n);
+  for (size_t j = 0; j < n; ++j) acc[j] = step_access(pr->steps[j]);
+  int64_t tail0 = -1;
+  for (size_t j = 0; j < n; ++j) {
+    std::vector<uint32_t> deps;
+    for (size_t i = 0; i < j; ++i)
+      if (accesses_conflict(acc[i], acc[j])) deps.push_back((uint32_t)i);
+    bool on_tail0 = tail0 < 0;
+    for (uint32_t i : deps) on_tail0 |= (int64_t)i == tail0;
+    const uint8_t sj = on_tail0 ? 0 : 1;
+    pr->stream_of[j] = sj;
+    if (sj == 0) tail0 = (int64_t)j;
+    // stream order covers same-stream dependencies and the other stream's earlier ones
+    // behind its latest: one wait at most
+    int64_t latest = -1;
+    for (uint32_t i : deps)
+      if (pr->stream_of[i] != sj) latest = std::max<int64_t>(latest, i);
+    if (latest >= 0) {
+      pr->wait_for[j].push_back((uint32_t)latest);
+      pr->record_after[latest] = 1;
+    }
+    if (sj == 1) {
+      pr->concurrent = true;
+      pr->side_steps++;
+    }
+  }
+}
+
+// Enqueues the status clear and every step: on stream s0 alone, or along the two-stream plan
+// (fork from s0, per-dependency events, join back into s0). Profiling runs use s0 alone so that
+// the per-step events bracket exactly one step each.
+hipError_t enqueue_steps(Program& pr, const Bound& b, hipStream_t s0, bool profile) {
+  hipError_t e = shk::launch_fill_u32(pr.status, 4, 0u, s0);
+  if (e != hipSuccess) return e;
+  if (!pr.concurrent || profile) {
+    for (size_t i = 0; i < pr.steps.size(); ++i) {
+      if (profile && (e = hipEventRecord(pr.events[i], s0)) != hipSuccess) return e;
+      if ((e = enqueue_step(pr, pr.steps[i], b, s0, pr.scratch)) != hipSuccess) return e;
+    }
+    if (profile) e = hipEventRecord(pr.events[pr.steps.size()], s0);
+    return e;
+  }
+  hipStream_t s1 = pr.ctx->side_stream;
+  if ((e = hipEventRecord(pr.fork, s0)) != hipSuccess || (e = hipStreamWaitEvent(s1, pr.fork, 0)) != hipSuccess)
+    return e;
+  for (size_t j = 0; j < pr.steps.size(); ++j) {
+    const bool side = pr.stream_of[j] != 0;
+    hipStream_t st = side ? s1 : s0;
+    for (uint32_t i : pr.wait_for[j])
+      if ((e = hipStreamWaitEvent(st, pr.step_done[i], 0)) != hipSuccess) return e;
+    if ((e = enqueue_step(pr, pr.steps[j], b, st, side ? pr.scratch_side : pr.scratch)) != hipSuccess)
+      return e;
+    if (pr.record_after[j] && (e = hipEventRecord(pr.step_done[j], st)) != hipSuccess) return e;
+  }
+  if ((e = hipEventRecord(pr.join, s1)) != hipSuccess) return e;
+  return hipStreamWaitEvent(s0, pr.join, 0);
+}
+
 int32_t finish_run_locked(Program* pr);
 
 void destroy_program(Program* p) {
@@ -668,6 +826,10 @@ void destroy_program(Program* p) {
   for (auto& kv : p->graph_cache) (void)hipGraphExecDestroy(kv.second);
   for (hipEvent_t e : p->events) (void)hipEventDestroy(e);
   if (p->done != nullptr) (void)hipEventDestroy(p->done);
+  for (hipEvent_t e : p->step_done)
+    if (e != nullptr) (void)hipEventDestroy(e);
+  if (p->fork != nullptr) (void)hipEventDestroy(p->fork);
+  if (p->join != nullptr) (void)hipEventDestroy(p->join);
   if (p->host_status != nullptr) (void)hipHostFree(p->host_status);
   if (p->arena != nullptr) (void)hipFree(p->arena);
   p->magic = 0;
@@ -1327,6 +1489,9 @@ int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_
     uint64_t off = 256;
     const uint64_t scratch_off = off;
     off += ((scratch_doubles * 8 + 255) / 256) * 256;
+    plan_streams(pr);
+    const uint64_t scratch_side_off = off;  // the side stream's own reduction scratch
+    if (pr->concurrent) off += ((scratch_doubles * 8 + 255) / 256) * 256;
     pr->internal_offset.assign(h.n_slots, 0);
     for (uint32_t i = 0; i < h.n_slots; ++i) {
       if (pr->slots[i].kind != SLOT_INTERNAL) continue;
@@ -1357,6 +1522,27 @@ int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_
     }
     pr->status = static_cast<uint32_t*>(pr->arena);
     pr->scratch = reinterpret_cast<double*>(static_cast<char*>(pr->arena) + scratch_off);
+    if (pr->concurrent) {
+      pr->scratch_side = reinterpret_cast<double*>(static_cast<char*>(pr->arena) + scratch_side_off);
+      bool ok = hipEventCreateWithFlags(&pr->fork, hipEventDisableTiming) == hipSuccess &&
+                hipEventCreateWithFlags(&pr->join, hipEventDisableTiming) == hipSuccess;
+      pr->step_done.assign(pr->steps.size(), nullptr);
+      for (size_t j = 0; ok && j < pr->steps.size(); ++j)
+        if (pr->record_after[j])
+          ok = hipEventCreateWithFlags(&pr->step_done[j], hipEventDisableTiming) == hipSuccess;
+      if (ok) {
+        std::lock_guard<std::mutex> lock(c->mutex);
+        if (c->side_stream == nullptr &&
+            hipStreamCreateWithFlags(&c->side_stream, hipStreamNonBlocking) != hipSuccess) {
+          c->side_stream = nullptr;
+          ok = false;
+        }
+      }
+      if (!ok) {
+        destroy_program(pr);
+        return fail(SHK_HIP_STATUS_NO_COMMAND_QUEUE, "side stream or event creation failed");
+      }
+    }
     pr->step_ms.assign(h.n_steps, 0.0);
     {
       const char* g = getenv("SHK_HIP_GRAPHS");
@@ -1401,6 +1587,31 @@ int32_t shk_hip_program_set_graph_mode(void* program, int32_t enabled) {
     if (st != SHK_HIP_STATUS_OK) return st;
   }
   pr->graphs = enabled != 0;
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_program_set_concurrent(void* program, int32_t enabled) {
+  Program* pr = checked<Program, kProgramMagic>(program);
+  if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
+  std::lock_guard<std::mutex> lock(pr->run_mutex);
+  if (pr->pending) {
+    const int32_t st = finish_run_locked(pr);
+    if (st != SHK_HIP_STATUS_OK) return st;
+  }
+  const bool want = enabled != 0 && pr->side_steps > 0;
+  if (want != pr->concurrent) {  // captured graphs embed the schedule
+    for (auto& kv : pr->graph_cache) (void)hipGraphExecDestroy(kv.second);
+    pr->graph_cache.clear();
+    pr->graph_order.clear();
+    pr->concurrent = want;
+  }
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_program_side_steps(void* program, uint32_t* out_steps) {
+  Program* pr = checked<Program, kProgramMagic>(program);
+  if (pr == nullptr || out_steps == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid arguments");
+  *out_steps = pr->concurrent ? pr->side_steps : 0;
   return SHK_HIP_STATUS_OK;
 }
 
@@ -1545,9 +1756,7 @@ int32_t run_program(void* program, uint32_t input_count, void* const* inputs, ui
         hipGraphExec_t exec = nullptr;
         bool ok = hipStreamBeginCapture(stream, hipStreamCaptureModeRelaxed) == hipSuccess;
         if (ok) {
-          bool steps_ok = shk::launch_fill_u32(pr->status, 4, 0u, stream) == hipSuccess;
-          for (size_t i = 0; steps_ok && i < pr->steps.size(); ++i)
-            steps_ok = enqueue_step(*pr, pr->steps[i], b, stream) == hipSuccess;
+          const bool steps_ok = enqueue_steps(*pr, b, stream, false) == hipSuccess;
           const bool ended = hipStreamEndCapture(stream, &graph) == hipSuccess;
           ok = steps_ok && ended && graph != nullptr &&
                hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess;
@@ -1576,17 +1785,12 @@ int32_t run_program(void* program, uint32_t input_count, void* const* inputs, ui
       }
     }
     if (!launched) {
-      HIP_TRY(shk::launch_fill_u32(pr->status, 4, 0u, stream));
-      for (size_t i = 0; i < pr->steps.size(); ++i) {
-        if (pr->profiling) HIP_TRY(hipEventRecord(pr->events[i], stream));
-        const hipError_t e = enqueue_step(*pr, pr->steps[i], b, stream);
-        if (e != hipSuccess) {
-          (void)hipStreamSynchronize(stream);
-          return fail(SHK_HIP_STATUS_EXECUTION_FAILED, "step %zu (opcode %u) launch failed: %s", i,
-                      pr->steps[i].rec.opcode, hipGetErrorName(e));
-        }
+      const hipError_t e = enqueue_steps(*pr, b, stream, pr->profiling);
+      if (e != hipSuccess) {
+        (void)hipStreamSynchronize(stream);
+        if (pr->ctx->side_stream != nullptr) (void)hipStreamSynchronize(pr->ctx->side_stream);
+        return fail(SHK_HIP_STATUS_EXECUTION_FAILED, "step launch failed: %s", hipGetErrorName(e));
       }
-      if (pr->profiling) HIP_TRY(hipEventRecord(pr->events[pr->steps.size()], stream));
     }
     HIP_TRY(hipMemcpyAsync(pr->host_status, pr->status, 4, hipMemcpyDeviceToHost, stream));
     HIP_TRY(hipEventRecord(pr->done, stream));

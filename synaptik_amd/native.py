@@ -63,6 +63,8 @@ EXPORTED_SYMBOLS = (
     "shk_hip_program_run",
     "shk_hip_program_run_async",
     "shk_hip_program_wait",
+    "shk_hip_program_set_concurrent",
+    "shk_hip_program_side_steps",
     "shk_hip_program_arena_bytes",
     "shk_hip_program_set_profiling",
     "shk_hip_program_step_times",
@@ -149,6 +151,8 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
             "shk_hip_program_run": (i32, [vp, u32, ctypes.POINTER(vp), u32, ctypes.POINTER(vp)]),
             "shk_hip_program_run_async": (i32, [vp, u32, ctypes.POINTER(vp), u32, ctypes.POINTER(vp)]),
             "shk_hip_program_wait": (i32, [vp]),
+            "shk_hip_program_set_concurrent": (i32, [vp, i32]),
+            "shk_hip_program_side_steps": (i32, [vp, ctypes.POINTER(u32)]),
             "shk_hip_program_arena_bytes": (i32, [vp, ctypes.POINTER(u64)]),
             "shk_hip_program_set_profiling": (i32, [vp, i32]),
             "shk_hip_program_step_times": (i32, [vp, ctypes.POINTER(ctypes.c_double), u32,
@@ -367,6 +371,16 @@ class HipProgram:
         ins = (ctypes.c_void_p * max(1, len(inputs)))(*[b.handle.value for b in inputs])
         outs = (ctypes.c_void_p * max(1, len(outputs)))(*[b.handle.value for b in outputs])
         check(self.lib, self.lib.shk_hip_program_run_async(self.handle, len(inputs), ins, len(outputs), outs))
+
+    def set_concurrent(self, enabled: bool) -> None:
+        """Two-stream step schedule on (the default) or off (`shk_hip_program_set_concurrent`)."""
+        check(self.lib, self.lib.shk_hip_program_set_concurrent(self.handle, 1 if enabled else 0))
+
+    def side_steps(self) -> int:
+        """Steps the active schedule runs on the context's second stream."""
+        v = ctypes.c_uint32()
+        check(self.lib, self.lib.shk_hip_program_side_steps(self.handle, ctypes.byref(v)))
+        return v.value
 
     def wait(self) -> None:
         """Completes the pending asynchronous run, raising its failure (`shk_hip_program_wait`)."""

@@ -145,7 +145,9 @@ __global__ void __launch_bounds__(256) gemm_small_k(GemmParams p, int vec_b, int
         float acc[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          float sum = a[i][0] * b[0][c];
+          // from +0, as the reference's sum starts (CpuMatmulReferenceKernel.java:34-119): a
+          // first product of -0 must not leave the result -0
+          float sum = fmaf(a[i][0], b[0][c], 0.0f);
 #pragma unroll
           for (int k = 1; k < KB; ++k) {
             const float t = fmaf(a[i][k], b[k][c], sum);

@@ -90,7 +90,7 @@ def cpu_baseline(sample_batch: int, seed=0) -> dict:
         "cores": 1,
         "kind": "port",
         "sample": (f"oracle forward+backward of MLP-4096 on {sample_batch} of the 4096 rows "
-                   f"({t_fb:.2f} s, scaled x{BATCH // sample_batch}) + one full SGD-momentum stage "
+                   f"({t_fb:.2f} s, scaled x{BATCH / sample_batch:.2f}) + one full SGD-momentum stage "
                    f"of all parameters ({t_upd:.2f} s): {step_s:.1f} s per 4096-sample step"),
     }
 
@@ -297,7 +297,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--cpu-sample", type=int, default=64, help="rows for the CPU baseline (0 = skip)")
+    ap.add_argument("--cpu-sample", type=int, default=192, help="rows for the CPU baseline (0 = skip)")
     ap.add_argument("--no-secondary", action="store_true", help="skip the C2/C3/C5 lines")
     ap.add_argument("--probe", action="store_true",
                     help="counter probe: 3 launches each of one 4096^3 NT GEMM and a 256 MiB copy")

@@ -873,6 +873,15 @@ int32_t shk_hip_context_create(int32_t device_ordinal, void** out_context) {
       delete c;
       return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "pinned status allocation failed");
     }
+    // The copy stream is created right after the compute stream, before any side stream, so
+    // that the runtime gives it a hardware queue of its own (queues are handed out in stream
+    // creation order): staged uploads must not queue behind compute work.
+    if (hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking) != hipSuccess) {
+      (void)hipHostFree(c->host_status);
+      (void)hipStreamDestroy(c->stream);
+      delete c;
+      return fail(SHK_HIP_STATUS_NO_COMMAND_QUEUE, "copy stream creation failed");
+    }
     *out_context = c;
     return SHK_HIP_STATUS_OK;
   } catch (const std::bad_alloc&) {
@@ -1598,13 +1607,8 @@ int32_t shk_hip_program_set_concurrent(void* program, int32_t enabled) {
     const int32_t st = finish_run_locked(pr);
     if (st != SHK_HIP_STATUS_OK) return st;
   }
-  const bool want = enabled != 0 && pr->side_steps > 0;
-  if (want != pr->concurrent) {  // captured graphs embed the schedule
-    for (auto& kv : pr->graph_cache) (void)hipGraphExecDestroy(kv.second);
-    pr->graph_cache.clear();
-    pr->graph_order.clear();
-    pr->concurrent = want;
-  }
+  // captured graphs embed the schedule; the graph cache key includes it, so both stay cached
+  pr->concurrent = enabled != 0 && pr->side_steps > 0;
   return SHK_HIP_STATUS_OK;
 }
 
@@ -1749,7 +1753,10 @@ int32_t run_program(void* program, uint32_t input_count, void* const* inputs, ui
     for (Buffer* x : bound) HIP_TRY(order_after_upload(x, stream));  // staged uploads landed
     bool launched = false;
     if (pr->graphs && !pr->profiling) {
-      auto it = pr->graph_cache.find(b.ptr);
+      // cache key: the bound pointers, then the schedule (one stream / two streams)
+      std::vector<void*> key(b.ptr);
+      key.push_back(reinterpret_cast<void*>(static_cast<uintptr_t>(pr->concurrent ? 2 : 1)));
+      auto it = pr->graph_cache.find(key);
       if (it == pr->graph_cache.end()) {
         // capture: status clear (a fill kernel, no memset node) + every step
         hipGraph_t graph = nullptr;
@@ -1772,8 +1779,8 @@ int32_t run_program(void* program, uint32_t input_count, void* const* inputs, ui
             }
             pr->graph_order.erase(pr->graph_order.begin());
           }
-          it = pr->graph_cache.emplace(b.ptr, exec).first;
-          pr->graph_order.push_back(b.ptr);
+          it = pr->graph_cache.emplace(key, exec).first;
+          pr->graph_order.push_back(key);
         } else {
           if (exec != nullptr) (void)hipGraphExecDestroy(exec);
           pr->graphs = false;

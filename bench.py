@@ -1,6 +1,6 @@
 """Headline benchmark: MLP-4096 training samples/s on one MI355X + GEMM fraction of fp32 MFMA peak.
 
-Workload ("Wide MLP-4096"): 4096 -> 4096 x4 hidden -> 4096, fp32, ReLU,
+Workload (benchmark configuration C4, "Wide MLP-4096"): 4096 -> 4096 x4 hidden -> 4096, fp32, ReLU,
 MSE loss, SGD momentum 0.9, batch 4096; X, Y ~ N(0,1), He-normal init from a seed; 10 warmup and
 100 timed steps by default. A step is one full training step of the device-resident program:
 5 forward GEMMs with fused bias+ReLU, the MSE loss and gradient, 5 dW GEMMs, 4 dX GEMMs with the
@@ -129,7 +129,7 @@ def probe() -> int:
 
 
 def secondary(ctx, reps: int = 5, cpu: bool = True) -> dict:
-    """The other BASELINE configs, measured on the same context (not the headline value)."""
+    """The other benchmark configurations, measured on the same context (not the headline value)."""
     from synaptik_amd.native import HipProgram
     from synaptik_amd.program import ProgramBuilder
     from synaptik_amd.training import (Adam, HipTrainingSession, MlpSpec, init_parameters,
@@ -309,7 +309,7 @@ def main() -> int:
         return probe()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this backend has no multi-GPU path "
-              "(see the sharding note in DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "(a data-parallel replica per GPU is the design); run with --gpus 1", file=sys.stderr)
         return 2
 
     from synaptik_amd.native import HipContext
@@ -416,7 +416,7 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "MLP-4096 training step (BASELINE configs[3])",
+        "config": {"workload": "MLP-4096 training step (benchmark configuration C4, configs[3])",
                    "layers": "4096->4096x4 hidden->4096 ReLU", "global_batch": BATCH,
                    "loss": "MSE mean", "optimizer": f"SGD lr={LR} momentum={MOMENTUM}",
                    "parallelism": "single GPU", "objective_after": loss},

@@ -1,6 +1,6 @@
 """Host-side mirror of the reference's backend SPI for the HIP backend.
 
-The reference's Java SPI (SURVEY: modules/planning, modules/prepare, modules/runtime) is:
+The reference's Java SPI (modules/planning, modules/prepare, modules/runtime) is:
   * BackendCapabilityProvider.supports(OperationCapabilityQuery)
         (modules/planning/.../capability/BackendCapabilityProvider.java:19-56) - pure, per node;
   * BackendPartitionPreparer.analyze(PrepareContext) -> BackendPartitionAnalysis(plan, requirements)

@@ -572,7 +572,7 @@ class HipTrainingSession:
 
 def lower_dense_layer(batch: int, fan_in: int, fan_out: int, activation: str | None = "relu",
                       weight_layout: str = "in_out"):
-    """One fused layer forward + backward with an upstream cotangent:
+    """One fused layer forward + backward with an upstream cotangent (benchmark configuration C2):
     Y = act(X . W + b) for W [in, out] (weight_layout "in_out", the config's X.W) or
     Y = act(X . W^T + b) for W [out, in] ("out_in", Linear's layout); returns Y, dX, dW, db.
 

@@ -1,4 +1,4 @@
-"""BASELINE configs at their full sizes on the GPU.
+"""The benchmark configurations at their full sizes on the GPU.
 
 C3 (784->1024->1024->10 ReLU, softmax-CE, Adam(1e-3, 0.9, 0.999, 1e-8), batch 1024) is compared
 with the oracle for 3 steps (the oracle's cost bounds the count). C4 (MLP-4096, batch 4096) is too

@@ -348,7 +348,7 @@ def test_optimizer_non_finite_leaves_state_untouched(ctx):
     assert bc.download(np.int64)[0] == 5
 
 
-# ---- BASELINE configs at full size ----
+# ---- benchmark configurations at full size ----
 def test_c2_fused_layer_forward_backward_full_size(ctx):
     """C2: Y = ReLU(X.W + b), X [8192,1024] ~ N(0,1), W [1024,1024] Xavier-uniform, b = 0,
     dY ~ N(0,1); Y, dX, dW, db vs the oracle (normwise relative error <= 1e-5; db exact sums)."""

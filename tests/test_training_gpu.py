@@ -1,6 +1,6 @@
 """Training-step parity on the GPU against the oracle's composition of the reference algorithms.
 
-Configs follow BASELINE.json: C1 (16->64->1 tanh, MSE, SGD 0.01, batch 256, 20 steps; loss
+Configurations follow the benchmark set: C1 (16->64->1 tanh, MSE, SGD 0.01, batch 256, 20 steps; loss
 trajectory within 1e-4 relative) and the C3 classifier architecture (784->1024->1024->10 ReLU,
 index softmax-CE, Adam) at a reduced batch so the oracle finishes in seconds. Closed-form known
 answers come from the reference's own tests.

@@ -29,23 +29,26 @@
 
 namespace shk {
 
+// The binary32 path alone: the caller guarantees t in [-87, 88].
+__host__ __device__ inline float exp_f32_in_range(float t) {
+  const float kLog2e = 0x1.715476p+0f;     // binary32(1 / ln 2)
+  const float kLn2Hi = 0x1.62e430p-1f;     // L1 = binary32(ln 2)
+  const float kLn2Lo = -0x1.05c610p-29f;   // L2 = binary32(ln 2 - L1)
+  const float n = rintf(t * kLog2e);
+  float r = fmaf(-n, kLn2Hi, t);  // exact
+  r = fmaf(-n, kLn2Lo, r);
+  float q = 0x1.a01a02p-13f;            // 1/7!
+  q = fmaf(q, r, 0x1.6c16c2p-10f);      // 1/6!
+  q = fmaf(q, r, 0x1.111112p-7f);       // 1/5!
+  q = fmaf(q, r, 0x1.555556p-5f);       // 1/4!
+  q = fmaf(q, r, 0x1.555556p-3f);       // 1/3!
+  q = fmaf(q, r, 0.5f);                 // 1/2!
+  const float s = fmaf(r * r, q, r);
+  return ldexpf(1.0f + s, (int)n);
+}
+
 __host__ __device__ inline float exp_f32(float t) {
-  if (t >= -87.0f && t <= 88.0f) {
-    const float kLog2e = 0x1.715476p+0f;     // binary32(1 / ln 2)
-    const float kLn2Hi = 0x1.62e430p-1f;     // L1 = binary32(ln 2)
-    const float kLn2Lo = -0x1.05c610p-29f;   // L2 = binary32(ln 2 - L1)
-    const float n = rintf(t * kLog2e);
-    float r = fmaf(-n, kLn2Hi, t);  // exact
-    r = fmaf(-n, kLn2Lo, r);
-    float q = 0x1.a01a02p-13f;            // 1/7!
-    q = fmaf(q, r, 0x1.6c16c2p-10f);      // 1/6!
-    q = fmaf(q, r, 0x1.111112p-7f);       // 1/5!
-    q = fmaf(q, r, 0x1.555556p-5f);       // 1/4!
-    q = fmaf(q, r, 0x1.555556p-3f);       // 1/3!
-    q = fmaf(q, r, 0.5f);                 // 1/2!
-    const float s = fmaf(r * r, q, r);
-    return ldexpf(1.0f + s, (int)n);
-  }
+  if (t >= -87.0f && t <= 88.0f) return exp_f32_in_range(t);
   return (float)exp((double)t);
 }
 

@@ -131,17 +131,36 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restric
   const float shift = (neg_inf && m == m) ? 0.0f : m;
   // One exponential per element: softmax keeps the rounded addends in registers and scales
   // them by the sum; log-softmax only needs the sum and recomputes x - shift.
+  //
+  // Every argument x - shift of a row shifted by its finite maximum lies in
+  // [fl(min - max), 0] (subtraction rounds monotonically), so when fl(min - max) >= -87 the
+  // whole row takes the binary32 path of the exponential without a per-element range test.
+  const bool in_range = shift == m && is_finite(m) && mn - m >= -87.0f;  // block-uniform
   float4 e[V];
   double s = 0.0;
+  if (in_range) {
 #pragma unroll
-  for (int i = 0; i < V; ++i) {
-    const int c = threadIdx.x + i * SM_NT;
-    if (c < C4) {
-      e[i].x = shifted_exp(v[i].x, shift);
-      e[i].y = shifted_exp(v[i].y, shift);
-      e[i].z = shifted_exp(v[i].z, shift);
-      e[i].w = shifted_exp(v[i].w, shift);
-      s += ((double)e[i].x + (double)e[i].y) + ((double)e[i].z + (double)e[i].w);
+    for (int i = 0; i < V; ++i) {
+      const int c = threadIdx.x + i * SM_NT;
+      if (c < C4) {
+        e[i].x = exp_f32_in_range(v[i].x - shift);
+        e[i].y = exp_f32_in_range(v[i].y - shift);
+        e[i].z = exp_f32_in_range(v[i].z - shift);
+        e[i].w = exp_f32_in_range(v[i].w - shift);
+        s += ((double)e[i].x + (double)e[i].y) + ((double)e[i].z + (double)e[i].w);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int c = threadIdx.x + i * SM_NT;
+      if (c < C4) {
+        e[i].x = shifted_exp(v[i].x, shift);
+        e[i].y = shifted_exp(v[i].y, shift);
+        e[i].z = shifted_exp(v[i].z, shift);
+        e[i].w = shifted_exp(v[i].w, shift);
+        s += ((double)e[i].x + (double)e[i].y) + ((double)e[i].z + (double)e[i].w);
+      }
     }
   }
   const float sum = (float)block_sum<SM_NT>(s, dl);

@@ -473,3 +473,33 @@ def test_single_op_kernel_matches_interpreter(ctx, op, n):
         (o,) = run_program(ctx, pb, [x, y], [so])
         outs.append(o.view(np.uint32))
     assert np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("C", [4096, 4092, 1000, 2048])
+@pytest.mark.parametrize("log", [False, True])
+def test_softmax_many_rows_special_rows(ctx, C, log):
+    """More rows than the device holds workgroups at once, so each workgroup of the row kernels
+    takes several rows (an odd or even count) and prefetches the next one; the special-value
+    rows sit at positions that fall on either LDS slot of a workgroup's row sequence."""
+    R = 3001
+    rng = np.random.default_rng(C * 7 + int(log))
+    x = (rng.standard_normal((R, C)) * 2).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] = 30.0
+    for base in (0, 1025, 2050, 2990):
+        x[base + 0, 1], x[base + 0, 3] = np.inf, np.nan
+        x[base + 1, :] = -np.abs(x[base + 1, :]); x[base + 1, 2] = 0.0
+        x[base + 2, :] = -np.abs(x[base + 2, :]) - 1; x[base + 2, 5] = -0.0
+        x[base + 3, 1] = np.inf
+        x[base + 4, 0] = -np.inf
+        x[base + 5, :] = -np.inf; x[base + 5, 3] = 80.0; x[base + 5, 7] = 85.0
+        x[base + 6, :] = np.nan
+    got, lse = gpu_softmax(ctx, x, log=log)
+    want = oracle.softmax_rows(x, log=log)
+    want_lse = oracle.logsumexp_rows(x)
+    for g_row, w_row in ((got, want), (lse[:, None], want_lse[:, None])):
+        nan_w = np.isnan(w_row)
+        assert np.array_equal(np.isnan(g_row), nan_w)
+        inf_w = np.isinf(w_row)
+        assert np.array_equal(g_row[inf_w], w_row[inf_w])
+        fin = ~nan_w & ~inf_w
+        np.testing.assert_allclose(g_row[fin], w_row[fin], rtol=2e-6, atol=2e-6 if log else 1e-30)

@@ -164,7 +164,9 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restric
     }
   }
   const float sum = (float)block_sum<SM_NT>(s, dl);
-  const float logsum = (float)log((double)sum);
+  // Every lane needs the binary64 logarithm of the sum only for log-softmax; softmax needs it
+  // only for the LSE output, which lane 0 forms below.
+  const float logsum = log_softmax ? (float)log((double)sum) : 0.0f;
   // Softmax scales by the reciprocal of the sum (one division per row; at most one extra
   // rounding per element against the reference's quotient). A sum whose reciprocal would leave
   // the normal range, or a non-finite one, keeps the per-element division.
@@ -195,7 +197,6 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restric
     }
   }
   if (lse != nullptr) {
-    float l = shift + logsum;
     if (neg_inf && is_finite(m)) {
       // LOG_SUM_EXP keeps the maximum as its shift even when the row holds -inf
       // (CpuLogSumExpEmitter.java:4-9); only the softmax values use the unshifted form.
@@ -207,9 +208,11 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restric
           s2 += ((double)shifted_exp(v[i].x, m) + (double)shifted_exp(v[i].y, m)) +
                 ((double)shifted_exp(v[i].z, m) + (double)shifted_exp(v[i].w, m));
       }
-      l = m + (float)log((double)(float)block_sum<SM_NT>(s2, dl));
+      const float sum2 = (float)block_sum<SM_NT>(s2, dl);
+      if (threadIdx.x == 0) lse[r] = m + (float)log((double)sum2);
+    } else if (threadIdx.x == 0) {
+      lse[r] = shift + (log_softmax ? logsum : (float)log((double)sum));
     }
-    if (threadIdx.x == 0) lse[r] = l;
   }
 }
 

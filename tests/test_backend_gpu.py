@@ -84,3 +84,46 @@ def test_prepared_executable_is_reusable_and_rejects_foreign_buffers(ctx):
     with pytest.raises(ValueError):
         exe.bind({"x": np.zeros(4)})
     exe.close()
+
+
+_GOLDEN = __import__("json").loads(
+    (__import__("pathlib").Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())
+
+
+def _golden_val(v):
+    if isinstance(v, str):
+        return {"inf": np.inf, "-inf": -np.inf, "nan": np.nan, "-0": -0.0}[v]
+    return float(v)
+
+
+@pytest.mark.parametrize("case", _GOLDEN["softmax_backward"],
+                         ids=lambda c: f"{'log' if c['log'] else 'softmax'}-{c['case']}")
+def test_softmax_backward_graph_reference_known_answers(ctx, case):
+    """The softmax / log-softmax gradient graphs as ReductionGradientRules.java:84-90 emits them
+    (MUL, keepdims SUM, SUB [, EXP]) through the SPI, bit for bit against
+    CpuSoftmaxBackwardConformanceTest's cases (saved outputs y and seeds g given; NaN payloads
+    free), non-finite operands included."""
+    y = np.array([_golden_val(v) for v in case["y"]], np.float32).reshape(2, 3)
+    g = np.array([_golden_val(v) for v in case["g"]], np.float32).reshape(2, 3)
+    if case["log"]:
+        v = {"y": f32(2, 3), "g": f32(2, 3), "e": f32(2, 3), "s": f32(2, 1), "es": f32(2, 3),
+             "dx": f32(2, 3)}
+        n = [Node("EXP", ["y"], "e"),
+             Node("SUM", ["g"], "s", {"axes": (1,), "keepdims": True}),
+             Node("MUL", ["e", "s"], "es"),
+             Node("SUB", ["g", "es"], "dx")]
+    else:
+        v = {"y": f32(2, 3), "g": f32(2, 3), "gy": f32(2, 3), "s": f32(2, 1), "gs": f32(2, 3),
+             "dx": f32(2, 3)}
+        n = [Node("MUL", ["g", "y"], "gy"),
+             Node("SUM", ["gy"], "s", {"axes": (1,), "keepdims": True}),
+             Node("SUB", ["g", "s"], "gs"),
+             Node("MUL", ["y", "gs"], "dx")]
+    exe = prepare(ctx, Partition(v, n, ["y", "g"], ["dx"]))
+    got = np.asarray(exe.run_values({"y": y, "g": g})["dx"], np.float32).ravel()
+    exe.close()
+    for i, w in enumerate(case["expected_bits"]):
+        if w is None:
+            assert np.isnan(got[i]), (i, got[i])
+        else:
+            assert int(got[i:i + 1].view(np.uint32)[0]) == w, (i, got[i])

@@ -167,6 +167,24 @@ def test_softmax_reference_known_answers(case, log):
             assert abs(g - w) <= case["tolerance"]
 
 
+def _bits_match(got, want_bits):
+    for i, (g, w) in enumerate(zip(np.asarray(got, np.float32).ravel(), want_bits)):
+        if w is None:
+            assert math.isnan(g), i
+        else:
+            assert int(np.array([g], np.float32).view(np.uint32)[0]) == w, (i, g)
+
+
+@pytest.mark.parametrize("case", [c for c in GOLDEN["softmax_backward"] if not c["log"]],
+                         ids=lambda c: c["case"])
+def test_softmax_backward_reference_known_answers(case):
+    """CpuSoftmaxBackwardConformanceTest's softmax rows, bit for bit (NaN payloads free)."""
+    y = np.array([_val(v) for v in case["y"]], np.float32).reshape(2, 3)
+    g = np.array([_val(v) for v in case["g"]], np.float32).reshape(2, 3)
+    with np.errstate(all="ignore"):
+        _bits_match(oracle.softmax_grad_rows(y, g), case["expected_bits"])
+
+
 def test_softmax_against_float64_and_invariants():
     rng = np.random.default_rng(4)
     x = (rng.standard_normal((64, 300)) * 2).astype(np.float32)

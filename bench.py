@@ -95,6 +95,46 @@ def cpu_baseline(sample_batch: int, seed=0) -> dict:
     }
 
 
+def openblas_baseline(threads: int, sample_batch: int, seed=0) -> dict:
+    """The reference's OpenBLAS route restated (OpenBlasGemmInvocation.java:41-68: sgemm on
+    row-major operands, single-threaded as qualifiedSingleThread, CpuBackendComposition.java:546-550)
+    with numpy's bundled OpenBLAS: the 14 GEMMs of an MLP-4096 step on `sample_batch` rows, scaled
+    to 4096 rows, plus ReLU, the MSE gradient and the SGD-momentum update in numpy. Reported beside
+    the reference's default (scalar) route; not the reference's own code."""
+    from threadpoolctl import threadpool_info, threadpool_limits
+    rng = np.random.default_rng(seed)
+    W = [rng.standard_normal((WIDTH, WIDTH), dtype=np.float32) * np.float32(0.02) for _ in range(LAYERS)]
+    b = [np.zeros(WIDTH, np.float32) for _ in range(LAYERS)]
+    x = rng.standard_normal((sample_batch, WIDTH), dtype=np.float32)
+    y = rng.standard_normal((sample_batch, WIDTH), dtype=np.float32)
+    with threadpool_limits(limits=threads, user_api="blas"):
+        _ = x @ W[0].T  # warm the BLAS thread pool and its buffers
+        t0 = time.perf_counter()
+        acts = [x]
+        for i in range(LAYERS):
+            z = acts[-1] @ W[i].T + b[i]
+            acts.append(np.maximum(z, 0) if i < LAYERS - 1 else z)
+        dz = (acts[-1] - y) * np.float32(2.0 / acts[-1].size)
+        grads = []
+        for i in reversed(range(LAYERS)):
+            grads.append((dz.T @ acts[i], dz.sum(0)))
+            if i > 0:
+                dz = (dz @ W[i]) * (acts[i] > 0)
+        t_fb = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        for (gw, gb), w, bb in zip(grads, reversed(W), reversed(b)):
+            for p, g in ((w, gw), (bb, gb)):
+                m = g.copy()            # first step: the momentum slot takes the gradient
+                p -= np.float32(LR) * m
+        t_upd = time.perf_counter() - t0
+    step_s = (BATCH / sample_batch) * t_fb + t_upd
+    version = next((i.get("version") for i in threadpool_info() if i["internal_api"] == "openblas"), None)
+    return {"value": BATCH / step_s, "unit": "samples/s", "threads": threads,
+            "kind": "openblas route (numpy's OpenBLAS %s), not the reference's default route" % version,
+            "sample": (f"{sample_batch} of the 4096 rows ({t_fb:.2f} s, scaled x{BATCH / sample_batch:.0f}) "
+                       f"+ one full SGD update ({t_upd:.2f} s)")}
+
+
 def probe() -> int:
     """Small fixed workload for rocprofv3 --pmc runs: FETCH_SIZE / WRITE_SIZE of the GEMM are
     scaled by the same counters read for a plain copy kernel of known size."""
@@ -401,6 +441,10 @@ def main() -> int:
     cpu = None
     if args.cpu_sample > 0:
         cpu = cpu_baseline(args.cpu_sample)
+        # the OpenBLAS route on one thread (as the reference qualifies it) and on the host's share
+        # of cores (16 per GPU on the benchmark boxes)
+        share = min(16, os.cpu_count() or 1)
+        cpu["openblas_route"] = [openblas_baseline(1, 256), openblas_baseline(share, 1024)]
         print(f"[bench] cpu baseline {cpu}", file=sys.stderr, flush=True)
 
     result = {

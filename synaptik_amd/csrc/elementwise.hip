@@ -207,6 +207,15 @@ __global__ void fill_u32_kernel(uint32_t* x, int64_t n, uint32_t v) {
        i += (int64_t)gridDim.x * blockDim.x)
     x[i] = v;
 }
+// Copies a program run's status word into the program's pinned host word and clears the device
+// word for the next run. One lane, ordinary (vector) stores.
+__global__ void status_publish_kernel(uint32_t* status, uint32_t* host_word) {
+  if (threadIdx.x == 0) {
+    const uint32_t v = status[0];
+    host_word[0] = v;
+    status[0] = 0u;
+  }
+}
 __global__ void copy_kernel(const float* __restrict__ s, float* __restrict__ d, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)
@@ -531,6 +540,10 @@ hipError_t launch_fill(float* x, int64_t n, float value, hipStream_t s) {
 hipError_t launch_fill_u32(uint32_t* x, int64_t n, uint32_t value, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(n, 4)), dim3(256), 0, s, x, n, value);
+  return hipGetLastError();
+}
+hipError_t launch_status_publish(uint32_t* status, uint32_t* host_word, hipStream_t s) {
+  hipLaunchKernelGGL(status_publish_kernel, dim3(1), dim3(64), 0, s, status, host_word);
   return hipGetLastError();
 }
 hipError_t launch_copy(const float* src, float* dst, int64_t n, hipStream_t s) {

@@ -203,6 +203,11 @@ struct Program {
   uint32_t* host_status = nullptr;
   hipEvent_t done = nullptr;
   bool pending = false;
+  // Every run ends with a kernel that copies the device status word into host_status and clears
+  // it, so the next run starts from a clear word without a fill of its own. Until a run has
+  // completed that way (a new program, a failed launch or execution) the next run clears the
+  // word first.
+  bool status_clear = false;
   // Two-stream schedule (plan_streams): step j runs on the context stream (0) or its side
   // stream (1, with scratch_side as its reduction scratch), first waiting for the events
   // recorded after the steps in wait_for[j]; record_after[j] marks steps other-stream steps
@@ -789,19 +794,18 @@ void plan_streams(Program* pr) {
   }
 }
 
-// Enqueues the status clear and every step: on stream s0 alone, or along the two-stream plan
-// (fork from s0, per-dependency events, join back into s0). Profiling runs use s0 alone so that
-// the per-step events bracket exactly one step each.
+// Enqueues every step, then the status publication (copy to host_status, clear): on stream s0
+// alone, or along the two-stream plan (fork from s0, per-dependency events, join back into s0).
+// Profiling runs use s0 alone so that the per-step events bracket exactly one step each.
 hipError_t enqueue_steps(Program& pr, const Bound& b, hipStream_t s0, bool profile) {
-  hipError_t e = shk::launch_fill_u32(pr.status, 4, 0u, s0);
-  if (e != hipSuccess) return e;
+  hipError_t e = hipSuccess;
   if (!pr.concurrent || profile) {
     for (size_t i = 0; i < pr.steps.size(); ++i) {
       if (profile && (e = hipEventRecord(pr.events[i], s0)) != hipSuccess) return e;
       if ((e = enqueue_step(pr, pr.steps[i], b, s0, pr.scratch)) != hipSuccess) return e;
     }
-    if (profile) e = hipEventRecord(pr.events[pr.steps.size()], s0);
-    return e;
+    if (profile && (e = hipEventRecord(pr.events[pr.steps.size()], s0)) != hipSuccess) return e;
+    return shk::launch_status_publish(pr.status, pr.host_status, s0);
   }
   hipStream_t s1 = pr.ctx->side_stream;
   if ((e = hipEventRecord(pr.fork, s0)) != hipSuccess || (e = hipStreamWaitEvent(s1, pr.fork, 0)) != hipSuccess)
@@ -816,7 +820,8 @@ hipError_t enqueue_steps(Program& pr, const Bound& b, hipStream_t s0, bool profi
     if (pr.record_after[j] && (e = hipEventRecord(pr.step_done[j], st)) != hipSuccess) return e;
   }
   if ((e = hipEventRecord(pr.join, s1)) != hipSuccess) return e;
-  return hipStreamWaitEvent(s0, pr.join, 0);
+  if ((e = hipStreamWaitEvent(s0, pr.join, 0)) != hipSuccess) return e;
+  return shk::launch_status_publish(pr.status, pr.host_status, s0);
 }
 
 int32_t finish_run_locked(Program* pr);
@@ -1668,8 +1673,10 @@ int32_t finish_run_locked(Program* pr) {
   if (!pr->pending) return SHK_HIP_STATUS_OK;
   const hipError_t se = hipEventSynchronize(pr->done);
   pr->pending = false;
-  if (se != hipSuccess)
+  if (se != hipSuccess) {
+    pr->status_clear = false;
     return fail(SHK_HIP_STATUS_EXECUTION_FAILED, "program execution failed: %s", hipGetErrorName(se));
+  }
   if (pr->profiling) {
     for (size_t i = 0; i < pr->steps.size(); ++i) {
       float ms = 0.f;
@@ -1751,6 +1758,12 @@ int32_t run_program(void* program, uint32_t input_count, void* const* inputs, ui
     std::vector<Buffer*> bound(in);
     bound.insert(bound.end(), out.begin(), out.end());
     for (Buffer* x : bound) HIP_TRY(order_after_upload(x, stream));  // staged uploads landed
+    if (!pr->status_clear) {
+      // not cleared by a completed run's publication; from here until this run completes, a
+      // failure leaves it unknown again
+      HIP_TRY(shk::launch_fill_u32(pr->status, 4, 0u, stream));
+    }
+    pr->status_clear = false;
     bool launched = false;
     if (pr->graphs && !pr->profiling) {
       // cache key: the bound pointers, then the schedule (one stream / two streams)
@@ -1758,7 +1771,7 @@ int32_t run_program(void* program, uint32_t input_count, void* const* inputs, ui
       key.push_back(reinterpret_cast<void*>(static_cast<uintptr_t>(pr->concurrent ? 2 : 1)));
       auto it = pr->graph_cache.find(key);
       if (it == pr->graph_cache.end()) {
-        // capture: status clear (a fill kernel, no memset node) + every step
+        // capture: every step + the status publication (kernels only, no memset or copy node)
         hipGraph_t graph = nullptr;
         hipGraphExec_t exec = nullptr;
         bool ok = hipStreamBeginCapture(stream, hipStreamCaptureModeRelaxed) == hipSuccess;
@@ -1799,9 +1812,9 @@ int32_t run_program(void* program, uint32_t input_count, void* const* inputs, ui
         return fail(SHK_HIP_STATUS_EXECUTION_FAILED, "step launch failed: %s", hipGetErrorName(e));
       }
     }
-    HIP_TRY(hipMemcpyAsync(pr->host_status, pr->status, 4, hipMemcpyDeviceToHost, stream));
     HIP_TRY(hipEventRecord(pr->done, stream));
     pr->pending = true;
+    pr->status_clear = true;  // once `done` completes without error
     if (async) {
       // a later staged upload into any bound buffer waits for this run (write-after-read)
       for (Buffer* x : bound) {

@@ -273,6 +273,43 @@ def test_index_cross_entropy_out_of_bounds_status(ctx, shape, with_grad):
         run_program(ctx, pb, [np.zeros(R * C, np.float32), y], outs)
 
 
+@pytest.mark.parametrize("mode", ["graph", "direct", "profiled", "async"])
+def test_status_word_does_not_leak_between_runs(ctx, mode):
+    """A run that flags the status word (an out-of-bounds target) fails; the next run of the same
+    program with valid targets succeeds with the right loss, and failing and succeeding runs
+    alternate (each run's status is published and cleared by its own last launch)."""
+    R, C = 64, 5
+    pb = ProgramBuilder()
+    sx, sy, sl = pb.input(R * C), pb.input(R, "i64"), pb.output(1)
+    pb.index_ce(sx, sy, sl, R, C)
+    prog = HipProgram(ctx, pb.image())
+    prog.set_graph_mode(mode == "graph")
+    prog.set_profiling(mode == "profiled")
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((R, C)).astype(np.float32)
+    good = rng.integers(0, C, R).astype(np.int64)
+    bad = good.copy()
+    bad[R - 1] = C
+    bx, bgood, bbad, bl = ctx.upload(x), ctx.upload(good), ctx.upload(bad), ctx.buffer(4)
+    want = oracle.index_ce_mean(x, good)
+
+    def run(labels):
+        if mode == "async":
+            prog.run_async([bx, labels], [bl])
+            prog.wait()
+        else:
+            prog.run([bx, labels], [bl])
+
+    for _ in range(3):
+        with pytest.raises(HipIndexError):
+            run(bbad)
+        run(bgood)
+        got = bl.download(np.float32, 1)[0]
+        assert abs(got - want) <= 1e-5 * abs(want)
+    run(bgood)
+    prog.close()
+
+
 # ---- optimizers ----
 def _opt_program(ctx, kind, n, **kw):
     pb = ProgramBuilder()

@@ -167,8 +167,10 @@ hipError_t launch_step_commit(int64_t* counter, const uint32_t* status, hipStrea
 
 hipError_t launch_fill(float* x, int64_t n, float value, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* x, int64_t n, uint32_t value, hipStream_t s);
-// Copies a run's status word to pinned host memory and clears it (the last launch of a run).
-hipError_t launch_status_publish(uint32_t* status, uint32_t* host_word, hipStream_t s);
+// Copies a run's status word to pinned host memory and clears it (the last launch of a run);
+// a non-null commit_counter first gets the step commit (incremented when the word is clear).
+hipError_t launch_status_publish(uint32_t* status, uint32_t* host_word, int64_t* commit_counter,
+                                 hipStream_t s);
 hipError_t launch_copy(const float* src, float* dst, int64_t n, hipStream_t s);
 // Canonical publication geometry of a strided view (element units, row-major ordinals).
 constexpr int CANONICAL_MAX_RANK = 16;

@@ -797,20 +797,28 @@ void plan_streams(Program* pr) {
 // Enqueues every step, then the status publication (copy to host_status, clear): on stream s0
 // alone, or along the two-stream plan (fork from s0, per-dependency events, join back into s0).
 // Profiling runs use s0 alone so that the per-step events bracket exactly one step each.
+// A program whose last step is the step commit has it performed by the publication kernel: the
+// commit reads the status word, so every step that can flag it precedes it, and nothing follows.
 hipError_t enqueue_steps(Program& pr, const Bound& b, hipStream_t s0, bool profile) {
   hipError_t e = hipSuccess;
+  const size_t n = pr.steps.size();
+  int64_t* commit = nullptr;
+  if (n > 0 && pr.steps[n - 1].rec.opcode == OP_STEP_COMMIT)
+    commit = b.get<int64_t>(pr.steps[n - 1].rec.slot[0]);
+  const size_t launched = commit != nullptr ? n - 1 : n;
   if (!pr.concurrent || profile) {
-    for (size_t i = 0; i < pr.steps.size(); ++i) {
+    for (size_t i = 0; i < n; ++i) {
       if (profile && (e = hipEventRecord(pr.events[i], s0)) != hipSuccess) return e;
-      if ((e = enqueue_step(pr, pr.steps[i], b, s0, pr.scratch)) != hipSuccess) return e;
+      if (i < launched && (e = enqueue_step(pr, pr.steps[i], b, s0, pr.scratch)) != hipSuccess)
+        return e;
     }
-    if (profile && (e = hipEventRecord(pr.events[pr.steps.size()], s0)) != hipSuccess) return e;
-    return shk::launch_status_publish(pr.status, pr.host_status, s0);
+    if (profile && (e = hipEventRecord(pr.events[n], s0)) != hipSuccess) return e;
+    return shk::launch_status_publish(pr.status, pr.host_status, commit, s0);
   }
   hipStream_t s1 = pr.ctx->side_stream;
   if ((e = hipEventRecord(pr.fork, s0)) != hipSuccess || (e = hipStreamWaitEvent(s1, pr.fork, 0)) != hipSuccess)
     return e;
-  for (size_t j = 0; j < pr.steps.size(); ++j) {
+  for (size_t j = 0; j < launched; ++j) {
     const bool side = pr.stream_of[j] != 0;
     hipStream_t st = side ? s1 : s0;
     for (uint32_t i : pr.wait_for[j])
@@ -821,7 +829,7 @@ hipError_t enqueue_steps(Program& pr, const Bound& b, hipStream_t s0, bool profi
   }
   if ((e = hipEventRecord(pr.join, s1)) != hipSuccess) return e;
   if ((e = hipStreamWaitEvent(s0, pr.join, 0)) != hipSuccess) return e;
-  return shk::launch_status_publish(pr.status, pr.host_status, s0);
+  return shk::launch_status_publish(pr.status, pr.host_status, commit, s0);
 }
 
 int32_t finish_run_locked(Program* pr);

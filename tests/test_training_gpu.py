@@ -185,3 +185,33 @@ def test_state_restore_replays_bit_exactly(ctx):
     for a, b in zip(second.weights + second.first + second.second, again.weights + again.first + again.second):
         assert np.array_equal(a, b)
     sess.close()
+
+
+def test_failed_two_stream_steps_leave_no_trace(ctx):
+    """A classifier step whose program runs on two streams (replayed graph; the step commit is
+    performed by the run's last launch) fails on an out-of-range label, then succeeds; two such
+    rounds leave exactly the state of a session that only ran the two clean steps."""
+    spec = MlpSpec.chain([64, 128, 128, 10], hidden="relu", loss="ce")
+    Ws, bs = init_parameters(spec, 3, "he_normal")
+    rng = np.random.default_rng(11)
+    x = rng.uniform(0, 1, (256, 64)).astype(np.float32)
+    good = rng.integers(0, 10, 256).astype(np.int64)
+    bad = good.copy()
+    bad[200] = 10
+    a = HipTrainingSession.open(ctx, spec, Ws, bs, Adam(1e-3), 256)
+    assert a.program.side_steps() > 0
+    for _ in range(2):
+        with pytest.raises(HipIndexError):
+            a.run(x, bad)
+        a.run(x, good)
+    b = HipTrainingSession.open(ctx, spec, Ws, bs, Adam(1e-3), 256)
+    b.run(x, good)
+    b.run(x, good)
+    sa, sb = a.state(), b.state()
+    assert sa.optimizer_steps == sb.optimizer_steps == 2
+    for p, q in zip(sa.weights + sa.biases + sa.first + sa.second,
+                    sb.weights + sb.biases + sb.first + sb.second):
+        assert np.array_equal(p.view(np.uint32), q.view(np.uint32))
+    assert a.objective().view(np.uint32) == b.objective().view(np.uint32)
+    a.close()
+    b.close()

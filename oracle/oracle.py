@@ -51,6 +51,7 @@ def lib():
             "shko_exact_sum": (f32, [F32P, i64, i64]),
             "shko_exact_mean": (f32, [F32P, i64, i64]),
             "shko_exact_quotient": (f32, [f32, i64]),
+            "shko_max": (f32, [F32P, i64, i64]),
             "shko_colsum": (None, [F32P, F32P, i64, i64, i64]),
             "shko_activation": (None, [i32, F32P, F32P, i64]),
             "shko_activation_grad": (None, [i32, F32P, F32P, F32P, i64]),
@@ -107,6 +108,18 @@ def exact_sum(x) -> np.float32:
 def exact_mean(x) -> np.float32:
     x = _c(x).ravel()
     return np.float32(lib().shko_exact_mean(_f(x), x.size, 1))
+
+
+def max_reduce(x) -> np.float32:
+    """MAX over every element of x (Java Math.max fold, AggregateReductionKind.java:128-137)."""
+    x = _c(x).ravel()
+    return np.float32(lib().shko_max(_f(x), x.size, 1))
+
+
+def max_rows(X) -> np.ndarray:
+    X = _c(X)
+    return np.array([lib().shko_max(_f(X[r]), X.shape[1], 1) for r in range(X.shape[0])],
+                    np.float32)
 
 
 def exact_quotient(value, count) -> np.float32:
@@ -327,7 +340,7 @@ class OracleMLP:
                dict(kind="adam"/"adamw", lr, beta1, beta2, eps, weight_decay).
     """
 
-    def __init__(self, weights, biases, acts, loss, optimizer, reduction="mean"):
+    def __init__(self, weights, biases, acts, loss, optimizer, reduction="mean", gemm="oracle"):
         self.W = [np.array(w, np.float32) for w in weights]
         self.b = [np.array(b, np.float32) for b in biases if b is not None]
         self.has_bias = [b is not None for b in biases]
@@ -338,12 +351,33 @@ class OracleMLP:
         self.m = [np.zeros_like(w) for w in self.W] + [np.zeros_like(b) for b in self.b]
         self.v = [np.zeros_like(w) for w in self.W] + [np.zeros_like(b) for b in self.b]
         self.steps = 0
+        # "oracle": the reference's sequential no-FMA GEMM (shko_matmul_f32); "float64": every
+        # GEMM evaluated in binary64 (numpy) and rounded once to binary32, for network sizes the
+        # scalar GEMM cannot finish in a test's time. All other operations are the oracle's.
+        if gemm not in ("oracle", "float64"):
+            raise ValueError(gemm)
+        self.gemm = gemm
+
+    def _mm(self, A, B, trans_a=False, trans_b=False):
+        if self.gemm == "oracle":
+            return matmul(A, B, trans_a=trans_a, trans_b=trans_b)
+        a = A.astype(np.float64)
+        b = B.astype(np.float64)
+        return np.ascontiguousarray((a.T if trans_a else a) @ (b.T if trans_b else b),
+                                    dtype=np.float32)
 
     def forward(self, x):
         xs = [_c(x)]
         bi = iter(self.b)
         for W, hb, a in zip(self.W, self.has_bias, self.acts):
-            xs.append(linear_forward(xs[-1], W, next(bi) if hb else None, a))
+            b = next(bi) if hb else None
+            if self.gemm == "oracle":
+                xs.append(linear_forward(xs[-1], W, b, a))
+            else:  # Z = X.W^T rounded, then + b in binary32, then the activation
+                z = self._mm(xs[-1], W, trans_b=True)
+                if b is not None:
+                    z = (z + b[None, :]).astype(np.float32)
+                xs.append(activation(a, z) if a else z)
         return xs
 
     def gradients(self, x, y):
@@ -358,10 +392,10 @@ class OracleMLP:
         L = len(self.W)
         gW, gb = [None] * L, [None] * L
         for l in reversed(range(L)):
-            gW[l] = matmul(dz, xs[l], trans_a=True)
+            gW[l] = self._mm(dz, xs[l], trans_a=True)
             gb[l] = colsum(dz) if self.has_bias[l] else None
             if l > 0:
-                dx = matmul(dz, self.W[l])
+                dx = self._mm(dz, self.W[l])
                 dz = activation_grad(self.acts[l - 1], dx, xs[l])
         return loss, gW, gb, xs
 

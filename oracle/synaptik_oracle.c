@@ -274,6 +274,16 @@ static float java_max(float a, float b) {
   return a > b ? a : b;
 }
 
+/* Floating MAX reduction (AggregateReductionKind.java:128-137): a left fold from the empty
+ * domain's -infinity with java_max above -- a NaN operand makes the result NaN (its payload is
+ * unspecified, foundational-modules.md:228), +0 is selected over -0, and values are compared
+ * as stored (the comparisons are exact, subnormals are never flushed). */
+float shko_max(const float* x, int64_t n, int64_t stride) {
+  float m = -INFINITY;
+  for (int64_t i = 0; i < n; ++i) m = java_max(m, x[i * stride]);
+  return m;
+}
+
 void shko_softmax_rows(const float* X, float* Y, int64_t R, int64_t C, int log_softmax) {
   for (int64_t r = 0; r < R; ++r) {
     const float* x = X + r * C;

@@ -11,6 +11,7 @@ void shko_matmul_f32(const float* A, const float* B, float* C, int64_t M, int64_
 float shko_exact_sum(const float* x, int64_t n, int64_t stride);
 float shko_exact_mean(const float* x, int64_t n, int64_t stride);
 float shko_exact_quotient(float value, int64_t count);
+float shko_max(const float* x, int64_t n, int64_t stride);
 void shko_colsum(const float* X, float* out, int64_t R, int64_t N, int64_t ldx);
 void shko_activation(int act, const float* x, float* y, int64_t n);
 void shko_activation_grad(int act, const float* g, const float* y, float* dx, int64_t n);

@@ -126,13 +126,15 @@ def test_row_reduce(ctx, kind):
     elif kind == "mean":
         want = np.array([oracle.exact_mean(r) for r in x], np.float32)
     elif kind == "max":
-        want = np.array([np.nan if np.isnan(r).any() else r.max() for r in x], np.float32)
+        want = oracle.max_rows(x)
     else:
         want = oracle.logsumexp_rows(x)
     fin = np.isfinite(want)
     assert np.array_equal(np.isnan(got), np.isnan(want))
     assert np.array_equal(got[~fin & ~np.isnan(want)], want[~fin & ~np.isnan(want)])
-    if kind in ("sum", "mean", "max"):
+    if kind == "max":  # a selection: bit-exact
+        assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))
+    elif kind in ("sum", "mean"):
         np.testing.assert_array_max_ulp(got[fin], want[fin], maxulp=1)
     else:
         np.testing.assert_allclose(got[fin], want[fin], rtol=1e-6)
@@ -147,8 +149,83 @@ def test_reduce_all(ctx, kind):
     sx, so = pb.input(n), pb.output(1)
     pb.reduce_all(sx, so, n, kind)
     (got,) = run_program(ctx, pb, [x], [so])
-    want = {"sum": oracle.exact_sum, "mean": oracle.exact_mean, "max": np.max}[kind](x)
-    np.testing.assert_array_max_ulp(got, np.array([want], np.float32), maxulp=1)
+    want = {"sum": oracle.exact_sum, "mean": oracle.exact_mean, "max": oracle.max_reduce}[kind](x)
+    if kind == "max":
+        assert got.view(np.uint32)[0] == np.array([want], np.float32).view(np.uint32)[0]
+    else:
+        np.testing.assert_array_max_ulp(got, np.array([want], np.float32), maxulp=1)
+
+
+def _max_special_rows(C):
+    """Rows whose MAX exercises Math.max's rules: signed-zero mixes (expect +0 when any +0),
+    all -0, NaN at the first / middle / last position, subnormal-only, -inf-only and an
+    infinity with NaN; every other row is random."""
+    rng = np.random.default_rng(C)
+    rows = []
+    z = np.where(rng.random(C) < 0.5, np.float32(-0.0), np.float32(0.0))
+    z[rng.integers(C)] = 0.0
+    rows.append(z)                                                   # -0/+0 mix -> +0
+    rows.append(np.full(C, -0.0, np.float32))                        # all -0 -> -0
+    neg = -np.abs(rng.standard_normal(C)).astype(np.float32) - 1.0
+    nz = neg.copy()
+    nz[rng.integers(C)] = -0.0
+    rows.append(nz)                                                  # negatives and one -0 -> -0
+    for pos in (0, C // 2, C - 1):
+        r = rng.standard_normal(C).astype(np.float32)
+        r[pos] = np.nan
+        rows.append(r)                                               # NaN anywhere -> NaN
+    sub = (rng.integers(1, 1 << 20, C).astype(np.uint32)).view(np.float32).copy()
+    sub[::3] *= -1
+    rows.append(sub)                                                 # subnormals, not flushed
+    rows.append(np.full(C, -np.inf, np.float32))
+    r = rng.standard_normal(C).astype(np.float32)
+    r[1] = np.inf
+    r[C - 2] = np.nan
+    rows.append(r)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("C", [5, 64, 3001, 70000])
+def test_row_max_math_max_rules_bit_exact(ctx, C):
+    x = _max_special_rows(C)
+    R = x.shape[0]
+    pb = ProgramBuilder()
+    sx, so = pb.input(R * C), pb.output(R)
+    pb.row_reduce(sx, so, R, C, "max")
+    (got,) = run_program(ctx, pb, [x], [so])
+    want = oracle.max_rows(x)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [1, 255, 256 * 1024 + 3, 3_000_001])
+@pytest.mark.parametrize("case", ["zeros-mixed", "zeros-neg", "nan-first", "nan-last",
+                                  "nan-middle", "subnormal", "neg-inf"])
+def test_reduce_all_max_math_max_rules_bit_exact(ctx, n, case):
+    """Whole-tensor MAX: both passes (per-block partials, then the fold over the partials)
+    must keep the signed-zero, NaN and subnormal rules."""
+    rng = np.random.default_rng(n)
+    if case.startswith("zeros"):
+        x = np.full(n, -0.0, np.float32)
+        if case == "zeros-mixed":
+            x[rng.integers(n)] = 0.0   # a single +0 in one block's partition
+    elif case.startswith("nan"):
+        x = rng.standard_normal(n).astype(np.float32)
+        x[{"nan-first": 0, "nan-last": n - 1, "nan-middle": n // 2}[case]] = np.nan
+    elif case == "subnormal":
+        x = -(rng.integers(1, 1 << 20, n).astype(np.uint32)).view(np.float32)
+    else:
+        x = np.full(n, -np.inf, np.float32)
+    pb = ProgramBuilder()
+    sx, so = pb.input(n), pb.output(1)
+    pb.reduce_all(sx, so, n, "max")
+    (got,) = run_program(ctx, pb, [x], [so])
+    want = oracle.max_reduce(x)
+    if np.isnan(want):
+        assert np.isnan(got[0])
+    else:
+        assert got.view(np.uint32)[0] == np.array([want], np.float32).view(np.uint32)[0]
 
 
 # ---- softmax / LSE ----

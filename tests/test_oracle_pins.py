@@ -117,6 +117,44 @@ def test_exact_sum_cancellation_and_subnormals():
     assert bits(oracle.exact_sum(np.array([-0.0, -0.0], np.float32))) == 0  # exact zero is +0
 
 
+def _bits32(v) -> int:
+    return int(np.array([v], np.float32).view(np.uint32)[0])
+
+
+@pytest.mark.parametrize("xs,want", [
+    ([], -math.inf),                       # empty domain: -infinity (AggregateReductionKind.java:133)
+    ([-0.0, 0.0], 0.0),                    # +0 is selected over -0, in either order
+    ([0.0, -0.0], 0.0),
+    ([-0.0, -0.0], -0.0),
+    ([-0.0], -0.0),                        # a singleton keeps its sign
+    ([-1e-45, -0.0, -3.0], -0.0),
+    ([1e-45, 2e-45, -1.0], 2e-45),         # subnormals compared as stored, never flushed
+    ([-2e-45, -1e-45], -1e-45),
+    ([-math.inf, -math.inf], -math.inf),
+    ([1.0, math.inf, 2.0], math.inf),
+    ([-FMAX, -math.inf], -FMAX),
+], ids=lambda v: str(v))
+def test_max_special_values(xs, want):
+    got = oracle.max_reduce(np.array(xs, np.float32))
+    assert _bits32(got) == _bits32(want)
+
+
+def test_max_propagates_nan_anywhere():
+    for pos in range(5):
+        x = np.array([1.0, -0.0, math.inf, 3.0, 0.0], np.float32)
+        x[pos] = math.nan
+        assert math.isnan(oracle.max_reduce(x))
+    assert math.isnan(oracle.max_reduce(np.array([math.nan, math.inf], np.float32)))
+
+
+def test_max_is_numpy_selection_without_zeros_or_nan():
+    rng = np.random.default_rng(9)
+    X = (rng.standard_normal((40, 1001)) * 100).astype(np.float32)
+    X[X == 0] = 1.0
+    assert np.array_equal(oracle.max_rows(X).view(np.uint32), X.max(axis=1).view(np.uint32))
+    assert _bits32(oracle.max_reduce(X)) == _bits32(X.max())
+
+
 def test_exact_quotient_is_rounded_once():
     for v, n in [(1.0, 3), (2.0, 7), (1e-38, 3), (123456.789, 4096 * 4096)]:
         q = oracle.exact_quotient(v, n)
@@ -327,8 +365,9 @@ def test_optimizer_stages_reject_non_finite():
 
 
 # ---- composition: MLP gradients vs torch autograd ----
+@pytest.mark.parametrize("gemm", ["oracle", "float64"])
 @pytest.mark.parametrize("loss,act", [("mse", "tanh"), ("mse", "relu"), ("ce", "relu"), ("mse", "sigmoid")])
-def test_mlp_gradients_against_torch_autograd(loss, act):
+def test_mlp_gradients_against_torch_autograd(loss, act, gemm):
     torch = pytest.importorskip("torch")
     from synaptik_amd.training import MlpSpec, init_parameters
     widths = [12, 20, 16, 5 if loss == "ce" else 3]
@@ -338,7 +377,7 @@ def test_mlp_gradients_against_torch_autograd(loss, act):
     rng = np.random.default_rng(12)
     x = rng.standard_normal((24, widths[0])).astype(np.float32)
     y = rng.integers(0, widths[-1], 24) if loss == "ce" else rng.standard_normal((24, widths[-1])).astype(np.float32)
-    model = oracle.OracleMLP(Ws, bs, [act, act, None], loss, dict(kind="sgd", lr=0.1))
+    model = oracle.OracleMLP(Ws, bs, [act, act, None], loss, dict(kind="sgd", lr=0.1), gemm=gemm)
     obj, gW, gb, _ = model.gradients(x, y)
     tW = [torch.tensor(w, dtype=torch.float64, requires_grad=True) for w in Ws]
     tb = [torch.tensor(b, dtype=torch.float64, requires_grad=True) for b in bs]
@@ -356,3 +395,30 @@ def test_mlp_gradients_against_torch_autograd(loss, act):
     assert abs(float(obj) - L.item()) <= 1e-5 * abs(L.item())
     for a, t in zip(gW + gb, tW + tb):
         np.testing.assert_allclose(a, t.grad.numpy(), rtol=1e-4, atol=1e-6)
+
+
+def test_float64_gemm_mode_tracks_the_oracle_gemm_over_steps():
+    """The binary64-GEMM composition (used where the scalar GEMM is too slow) follows the
+    reference-order composition over several Adam and SGD-momentum steps within the parity
+    tolerance, and its integer-operand GEMMs are bit-identical (exact sums)."""
+    from synaptik_amd.training import MlpSpec, init_parameters
+    spec = MlpSpec.chain([40, 64, 48, 10], hidden="relu", loss="ce")
+    Ws, bs = init_parameters(spec, 5, "he_normal")
+    rng = np.random.default_rng(6)
+    x = rng.uniform(0, 1, (96, 40)).astype(np.float32)
+    y = rng.integers(0, 10, 96)
+    for opt in (dict(kind="adam", lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8),
+                dict(kind="sgd", lr=0.05, momentum=0.9)):
+        a = oracle.OracleMLP(Ws, bs, ["relu", "relu", None], "ce", opt)
+        b = oracle.OracleMLP(Ws, bs, ["relu", "relu", None], "ce", opt, gemm="float64")
+        la = [float(a.step(x, y)) for _ in range(10)]
+        lb = [float(b.step(x, y)) for _ in range(10)]
+        np.testing.assert_allclose(lb, la, rtol=1e-5)
+        for u, v in zip(a.W + a.b, b.W + b.b):
+            assert np.linalg.norm(u - v) <= 1e-5 * np.linalg.norm(u)
+    A = rng.integers(-3, 4, (33, 70)).astype(np.float32)
+    B = rng.integers(-3, 4, (70, 21)).astype(np.float32)
+    m = oracle.OracleMLP(Ws, bs, ["relu", "relu", None], "ce", {"kind": "sgd", "lr": 0.1},
+                         gemm="float64")
+    assert np.array_equal(m._mm(A, B), oracle.matmul(A, B))
+    assert np.array_equal(m._mm(A.T.copy(), B, trans_a=True), oracle.matmul(A, B))

@@ -133,3 +133,56 @@ def test_pipelined_training_stops_at_a_failed_step(ctx):
     assert s.optimizer_steps == 3
     ref.close()
     s.close()
+
+
+def test_mismatched_batches_raise_and_change_nothing(ctx):
+    spec = MlpSpec.chain([4, 8, 1], hidden="relu", loss="mse")
+    Ws, bs = init_parameters(spec, 0, "he_normal")
+    x = np.ones((8, 4), np.float32)
+    good = (x, np.zeros((8, 1), np.float32))
+    s = HipTrainingSession.open(ctx, spec, Ws, bs, Sgd(0.1, momentum=0.9), 8)
+    s.run(*good)
+    before = _bits(s.state())
+    short = (x[:6], np.zeros((6, 1), np.float32))  # a short final batch
+    wide = (np.ones((8, 5), np.float32), np.zeros((8, 1), np.float32))
+    for bad in (short, wide):
+        with pytest.raises(ValueError):
+            s.run(*bad)
+        with pytest.raises(ValueError):
+            s.run_pipelined([good, bad, good])  # checked before the first run
+    assert s.optimizer_steps == 1
+    for u, v in zip(before, _bits(s.state())):
+        assert np.array_equal(u, v)
+    s.close()
+
+
+def test_staging_failure_after_a_committed_run_keeps_that_run(ctx, monkeypatch):
+    """The next batch's staging raises while step 1 is pending: step 1 still commits on the
+    device, so the session must adopt its candidate set before the error propagates."""
+    spec = MlpSpec.chain([4, 8, 1], hidden="relu", loss="mse")
+    Ws, bs = init_parameters(spec, 0, "he_normal")
+    x = np.ones((8, 4), np.float32)
+    good = (x, np.zeros((8, 1), np.float32))
+    ref = HipTrainingSession.open(ctx, spec, Ws, bs, Sgd(0.1, momentum=0.9), 8)
+    ref.run(*good)
+    s = HipTrainingSession.open(ctx, spec, Ws, bs, Sgd(0.1, momentum=0.9), 8)
+    s.run(*good)  # creates the session's batch buffers
+    s._x2 = s.ctx.buffer(s._x.nbytes)
+    s._y2 = s.ctx.buffer(s._y.nbytes)
+
+    def refuse(*a, **k):
+        raise RuntimeError("staging refused")
+
+    monkeypatch.setattr(s._x2, "upload_staged", refuse)
+    ref.run(*good)
+    with pytest.raises(RuntimeError, match="staging refused"):
+        s.run_pipelined([good, good])
+    assert s.optimizer_steps == ref.optimizer_steps == 2
+    for u, v in zip(_bits(ref.state()), _bits(s.state())):
+        assert np.array_equal(u, v)
+    s.run(*good)
+    ref.run(*good)
+    for u, v in zip(_bits(ref.state()), _bits(s.state())):
+        assert np.array_equal(u, v)
+    ref.close()
+    s.close()

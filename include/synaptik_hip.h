@@ -11,6 +11,8 @@
  *     out-pointer on entry;
  *   - handles are opaque, owned by the caller's wrapper and released exactly once;
  *   - calls may come from any thread; a context serializes the work it enqueues on its stream;
+ *     concurrent runs of one program are isolated: each holds a per-run lease of its own (see
+ *     shk_hip_program_create);
  *   - a program run is synchronous: device work is complete when it returns
  *     (docs/architecture/contracts/backend-execution.md:1658-1660).
  * The last error message of the calling thread is available through shk_hip_last_error().
@@ -141,9 +143,18 @@ int32_t shk_hip_buffer_download_storage(void* buffer, uint32_t element_width, in
                                         void* destination, uint64_t destination_capacity);
 
 /* Programs: an op-list image (the HIP analogue of the Metal graph image decoded by
- * synaptik_metal_mpsgraph_executable_create, synaptik_metal_foundation.m:8573). The program
- * owns a device arena for its internal slots and scratch, allocated once here and reused by
- * every run. Image layout: synaptik_amd/program.py (ProgramImage) and runtime.cpp. */
+ * synaptik_metal_mpsgraph_executable_create, synaptik_metal_foundation.m:8573). The decoded
+ * program is immutable and shared by every run, as the reference's PreparedExecutable is
+ * (PreparedExecutable.java:58-186). Per-run state -- a device arena with the internal slots,
+ * the reduction scratch and the status word, plus the run's events and captured HIP graphs --
+ * lives in leases owned by the program, the analogue of RunState-owned buffers and workspaces
+ * (docs/backend-guide/writing-a-backend.md:140-142): a run holds one lease until its
+ * completion is observed, and concurrent runs hold different leases, so their results are those
+ * of running them one after another (Engine.java:480-507). The first lease is allocated here;
+ * a run that finds every lease held creates another, up to 4 per program (SHK_HIP_MAX_LEASES,
+ * 1..64, read here), and beyond that waits for one to be returned. A lease's internal slots
+ * start zeroed and keep what its last run left. Image layout: synaptik_amd/program.py and
+ * runtime.cpp. */
 int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_bytes,
                                void** out_program);
 int32_t shk_hip_program_release(void* program);
@@ -151,13 +162,16 @@ int32_t shk_hip_program_release(void* program);
  * validates sizes and aliasing (INCOMPATIBLE_RESOURCE), enqueues every step, waits, and maps
  * the device status word (ARITHMETIC, INDEX_OUT_OF_BOUNDS). Replaces
  * synaptik_metal_mpsgraph_executable_run (synaptik_metal_foundation.m:9984-10083).
- * Concurrent runs of one program serialize on its arena. */
+ * Runs from several threads proceed concurrently on different leases; their kernels are
+ * enqueued on the context's streams one run after another. */
 int32_t shk_hip_program_run(void* program, uint32_t input_count, void* const* inputs,
                             uint32_t output_count, void* const* outputs);
 /* shk_hip_program_run without the wait: binds, validates and enqueues the run, then returns;
- * shk_hip_program_wait completes it and maps its status word exactly as shk_hip_program_run
- * would. A run, set_profiling, set_graph_mode or step_times call on a program whose
- * asynchronous run is pending first waits for it, and returns that run's failure if it failed.
+ * shk_hip_program_wait completes every pending asynchronous run of the program, oldest first,
+ * and maps their status words exactly as shk_hip_program_run would (the first failure is
+ * returned). A run, set_profiling, set_graph_mode, set_concurrent or step_times call on a
+ * program with pending asynchronous runs first completes them, and returns the first failure
+ * among them without doing anything else.
  * HIP addition (the reference's BoundInvocation.executeBound is synchronous): it lets a host
  * batch upload (shk_hip_buffer_upload_staged) overlap the previous run. */
 int32_t shk_hip_program_run_async(void* program, uint32_t input_count, void* const* inputs,
@@ -172,8 +186,11 @@ int32_t shk_hip_program_wait(void* program);
  * side_steps reports how many steps the active plan puts on the second stream. */
 int32_t shk_hip_program_set_concurrent(void* program, int32_t enabled);
 int32_t shk_hip_program_side_steps(void* program, uint32_t* out_steps);
-/* Arena bytes owned by the program (internal slots + scratch). */
+/* Arena bytes of one lease (internal slots + scratch + status word). */
 int32_t shk_hip_program_arena_bytes(void* program, uint64_t* out_bytes);
+/* Number of leases the program has created (1 after create; more after concurrent runs).
+ * HIP addition for observability. */
+int32_t shk_hip_program_lease_count(void* program, uint32_t* out_leases);
 /* Per-step device timing with HIP events on the context stream. Enabling clears the totals. */
 int32_t shk_hip_program_set_profiling(void* program, int32_t enabled);
 /* Writes min(capacity, steps) accumulated milliseconds per step and the number of profiled runs. */

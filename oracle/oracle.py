@@ -62,6 +62,7 @@ def lib():
             "shko_logsumexp_grad_rows": (None, [F32P, F32P, F32P, F32P, i64, i64]),
             "shko_mse_mean": (f32, [F32P, F32P, i64]),
             "shko_mse_sum": (f32, [F32P, F32P, i64]),
+            "shko_mse_mean_exact": (f32, [F32P, F32P, i64]),
             "shko_mse_grad": (None, [F32P, F32P, F32P, i64, f32, i32]),
             "shko_index_ce_mean": (i32, [F32P, I64P, i64, i64, i32, i64, F32P]),
             "shko_index_ce_grad": (None, [F32P, I64P, F32P, i64, i64, i32, i64, f32]),
@@ -69,6 +70,7 @@ def lib():
                                      i32, i64]),
             "shko_adam_stage": (i32, [F32P, F32P, F32P, F32P, F32P, F32P, F32P, i64, f32, f32,
                                       f32, f32, f32, i32, i64]),
+            "shko_adam_apply": (i32, [F32P, F32P, F32P, F32P, i64, f32, f32, f32, f32, f32, i32, i64]),
             "shko_canonical_bytes": (i32, [ctypes.c_void_p, ctypes.c_uint64, i32, i32, i32, I64P,
                                            I64P, i64, ctypes.c_void_p]),
         }
@@ -190,6 +192,12 @@ def mse_mean(p, t) -> np.float32:
     return np.float32(lib().shko_mse_mean(_f(p), _f(t), p.size))
 
 
+def mse_mean_exact(p, t) -> np.float32:
+    """MSE MEAN with the contract's exact reduction (shko_mse_mean_exact)."""
+    p, t = _c(p).ravel(), _c(t).ravel()
+    return np.float32(lib().shko_mse_mean_exact(_f(p), _f(t), p.size))
+
+
 def mse_sum(p, t) -> np.float32:
     p, t = _c(p).ravel(), _c(t).ravel()
     return np.float32(lib().shko_mse_sum(_f(p), _f(t), p.size))
@@ -249,6 +257,19 @@ def adam_stage(p, g, m, v, *, lr, beta1, beta2, eps, weight_decay=0.0, decoupled
     if rc:
         raise ArithmeticError("Adam intermediate or candidate is not finite")
     return pc, mc, vc
+
+
+def adam_apply(p, m_new, v_new, *, lr, beta1, beta2, eps, weight_decay=0.0, decoupled=False,
+               completed_steps=0):
+    """Adam's parameter candidates from given new moments (the arithmetic after the moment
+    updates in stageAdaptiveElement32, TrainingParameter.java:433-525)."""
+    p, m_new, v_new = _c(p), _c(m_new), _c(v_new)
+    pc = p.copy()
+    rc = lib().shko_adam_apply(_f(p), _f(m_new), _f(v_new), _f(pc), p.size, lr, beta1, beta2,
+                               eps, weight_decay, int(decoupled), int(completed_steps))
+    if rc:
+        raise ArithmeticError("Adam intermediate or candidate is not finite")
+    return pc
 
 
 # ---- MLP training step ----
@@ -340,7 +361,8 @@ class OracleMLP:
                dict(kind="adam"/"adamw", lr, beta1, beta2, eps, weight_decay).
     """
 
-    def __init__(self, weights, biases, acts, loss, optimizer, reduction="mean", gemm="oracle"):
+    def __init__(self, weights, biases, acts, loss, optimizer, reduction="mean", gemm="oracle",
+                 mse_sum="sequential"):
         self.W = [np.array(w, np.float32) for w in weights]
         self.b = [np.array(b, np.float32) for b in biases if b is not None]
         self.has_bias = [b is not None for b in biases]
@@ -357,6 +379,11 @@ class OracleMLP:
         if gemm not in ("oracle", "float64"):
             raise ValueError(gemm)
         self.gemm = gemm
+        # "sequential": the reference CPU kernels' binary32 running sum of the squares;
+        # "exact": the Model contract's exact reduction (mse_mean_exact). MEAN reduction only.
+        if mse_sum not in ("sequential", "exact"):
+            raise ValueError(mse_sum)
+        self.mse_sum = mse_sum
 
     def _mm(self, A, B, trans_a=False, trans_b=False):
         if self.gemm == "oracle":
@@ -384,14 +411,19 @@ class OracleMLP:
         xs = self.forward(x)
         pred = xs[-1]
         if self.loss == "mse":
-            loss = mse_mean(pred, y) if self.reduction == "mean" else mse_sum(pred, y)
+            if self.reduction == "mean":
+                loss = mse_mean_exact(pred, y) if self.mse_sum == "exact" else mse_mean(pred, y)
+            else:
+                loss = mse_sum(pred, y)
             dz = mse_grad(pred, y, reduction=self.reduction)
         else:
             loss = index_ce_mean(pred, y)
             dz = index_ce_grad(pred, y)
         L = len(self.W)
         gW, gb = [None] * L, [None] * L
+        self.last_cotangents = [None] * L  # dZ_l of the last gradients() call, per layer
         for l in reversed(range(L)):
+            self.last_cotangents[l] = dz
             gW[l] = self._mm(dz, xs[l], trans_a=True)
             gb[l] = colsum(dz) if self.has_bias[l] else None
             if l > 0:
@@ -401,7 +433,8 @@ class OracleMLP:
 
     def step(self, x, y):
         """One training step; returns the objective. Raises ArithmeticError without commit."""
-        loss, gW, gb, _ = self.gradients(x, y)
+        loss, gW, gb, xs = self.gradients(x, y)
+        self.last_inputs, self.last_gradients = xs, gW + [g for g in gb if g is not None]
         params = self.W + self.b
         grads = gW + [g for g in gb if g is not None]
         o = self.opt

@@ -383,6 +383,24 @@ float shko_mse_mean(const float* p, const float* t, int64_t n) {
   return shko_exact_quotient(sum, n);
 }
 
+/* MSE MEAN as the Model contract states it (foundational-modules.md:343: one subtraction and
+ * delta*delta per position, "then its exact reduction and optional divisor"): the binary32
+ * squares summed exactly and divided by n with one rounding. The reference's CPU kernels sum
+ * the squares sequentially in binary32 instead (shko_mse_mean above; the generated kernel
+ * CpuLossEmitter.emitContiguousMseInt:879-935 does the same), which drifts from this once the
+ * running sum's ulp approaches the squares. */
+float shko_mse_mean_exact(const float* p, const float* t, int64_t n) {
+  if (n == 0) return NAN;
+  superacc s;
+  sa_init(&s);
+  for (int64_t i = 0; i < n; ++i) {
+    float d = p[i] - t[i];
+    float sq = d * d;
+    sa_add(&s, sq);
+  }
+  return sa_result(&s, n);
+}
+
 /* meanSquaredError(float[], float[], SUM): the sequential binary32 sum itself. */
 float shko_mse_sum(const float* p, const float* t, int64_t n) {
   float sum = 0.0f;
@@ -518,6 +536,9 @@ int shko_sgd_stage(const float* p, const float* g, const float* m, float* p_out,
   return 0;
 }
 
+static int adam_tail(float base, float first, float second, float c1, float c2, float lr,
+                     float eps, float* out);
+
 /* stageAdaptive32 / stageAdaptiveElement32 :433-525; decoupled = AdamW. */
 int shko_adam_stage(const float* p, const float* g, const float* m, const float* v, float* p_out,
                     float* m_out, float* v_out, int64_t n, float lr, float b1, float b2, float eps,
@@ -562,23 +583,63 @@ int shko_adam_stage(const float* p, const float* g, const float* m, const float*
     FIN(sg);
     float second = st + sg;
     FIN(second);
-    float cf = first / c1;
-    float cs = second / c2;
-    FIN(cf);
-    FIN(cs);
-    float root = (float)sqrt((double)cs);
-    FIN(root);
-    float denom = root + eps;
-    if (!isfinite(denom) || denom <= 0.0f) return 1;
-    float numer = lr * cf;
-    FIN(numer);
-    float update = numer / denom;
-    FIN(update);
-    float cand = base - update;
-    FIN(cand);
+    float cand;
+    if (adam_tail(base, first, second, c1, c2, lr, eps, &cand)) return 1;
     m_out[i] = first;
     v_out[i] = second;
     p_out[i] = cand;
+  }
+  return 0;
+}
+
+/* The parameter candidate of one Adam element from its new moments (the tail of
+ * stageAdaptiveElement32): p_out = base - (lr * (first / c1)) / ((float)sqrt(second / c2) + eps),
+ * with the same finiteness checks. Shared by shko_adam_stage and shko_adam_apply. */
+static int adam_tail(float base, float first, float second, float c1, float c2, float lr,
+                     float eps, float* out) {
+  float cf = first / c1;
+  float cs = second / c2;
+  FIN(cf);
+  FIN(cs);
+  float root = (float)sqrt((double)cs);
+  FIN(root);
+  float denom = root + eps;
+  if (!isfinite(denom) || denom <= 0.0f) return 1;
+  float numer = lr * cf;
+  FIN(numer);
+  float update = numer / denom;
+  FIN(update);
+  float cand = base - update;
+  FIN(cand);
+  *out = cand;
+  return 0;
+}
+
+/* Adam's parameter candidates from given new moments m_new, v_new (for checking a device's
+ * update arithmetic independently of its gradient): the base is p (coupled decay) or
+ * p * (1 - lr * decay) (decoupled), then adam_tail. Returns 1 on a non-finite intermediate. */
+int shko_adam_apply(const float* p, const float* m_new, const float* v_new, float* p_out,
+                    int64_t n, float lr, float b1, float b2, float eps, float decay,
+                    int decoupled, int64_t completed_steps) {
+  const int64_t step = completed_steps + 1;
+  float c1 = 1.0f - (float)pow((double)b1, (double)step);
+  float c2 = 1.0f - (float)pow((double)b2, (double)step);
+  if (!isfinite(c1) || c1 <= 0.0f || !isfinite(c2) || c2 <= 0.0f) return 1;
+  float decay_factor = 1.0f;
+  if (decoupled) {
+    float scale = lr * decay;
+    FIN(scale);
+    decay_factor -= scale;
+    FIN(decay_factor);
+  }
+  for (int64_t i = 0; i < n; ++i) {
+    float base = p[i];
+    FIN(base);
+    if (decoupled) {
+      base = base * decay_factor;
+      FIN(base);
+    }
+    if (adam_tail(base, m_new[i], v_new[i], c1, c2, lr, eps, &p_out[i])) return 1;
   }
   return 0;
 }

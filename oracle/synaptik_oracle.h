@@ -23,6 +23,7 @@ void shko_softmax_grad_rows(const float* Y, const float* G, float* DX, int64_t R
 void shko_logsumexp_grad_rows(const float* X, const float* lse, const float* g, float* DX,
                               int64_t R, int64_t C);
 float shko_mse_mean(const float* p, const float* t, int64_t n);
+float shko_mse_mean_exact(const float* p, const float* t, int64_t n);
 float shko_mse_sum(const float* p, const float* t, int64_t n);
 void shko_mse_grad(const float* p, const float* t, float* grad, int64_t n, float g, int sum);
 int shko_index_ce_mean(const float* logits, const int64_t* target, int64_t R, int64_t C,
@@ -32,6 +33,9 @@ void shko_index_ce_grad(const float* logits, const int64_t* target, float* grad,
 int shko_sgd_stage(const float* p, const float* g, const float* m, float* p_out, float* m_out,
                    int64_t n, float lr, float momentum, float dampening, float weight_decay,
                    int nesterov, int has_momentum_slot, int64_t completed_steps);
+int shko_adam_apply(const float* p, const float* m_new, const float* v_new, float* p_out,
+                    int64_t n, float lr, float b1, float b2, float eps, float decay,
+                    int decoupled, int64_t completed_steps);
 int shko_adam_stage(const float* p, const float* g, const float* m, const float* v, float* p_out,
                     float* m_out, float* v_out, int64_t n, float lr, float b1, float b2, float eps,
                     float decay, int decoupled, int64_t completed_steps);

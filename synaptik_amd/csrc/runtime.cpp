@@ -18,6 +18,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <condition_variable>
 #include <mutex>
 #include <new>
 #include <string>
@@ -178,47 +179,63 @@ struct Step {
   std::vector<uint8_t> payload;
 };
 
+// Per-run state of a program (the analogue of the reference's RunState-owned buffers and
+// workspaces, docs/backend-guide/writing-a-backend.md:140-142): a device arena holding the
+// status word, the reduction scratch of each stream and the internal slots, a pinned host word
+// the run's status is published to, the events of one run, and the HIP graphs captured over this
+// arena. A run holds one lease from acquisition until its completion is observed; concurrent runs
+// of one program hold different leases, so nothing one run writes is visible to another.
+struct Lease {
+  void* arena = nullptr;
+  uint32_t* status = nullptr;      // device status word (first bytes of the arena)
+  double* scratch = nullptr;       // reduction partials of the context stream's steps
+  double* scratch_side = nullptr;  // ... of the side stream's steps (two-stream plan)
+  uint32_t* host_status = nullptr; // pinned; written by the run's status publication kernel
+  hipEvent_t done = nullptr;       // end of the run
+  hipEvent_t fork = nullptr, join = nullptr;
+  std::vector<hipEvent_t> step_done;  // per step the other stream waits for
+  std::vector<hipEvent_t> events;     // per-step timing (profiled runs), created on first use
+  // HIP-graph replay: the step sequence captured once per distinct set of bound pointers and
+  // schedule (up to 8 cached, oldest evicted)
+  std::map<std::vector<void*>, hipGraphExec_t> graph_cache;
+  std::vector<std::vector<void*>> graph_order;
+  bool graphs_ok = true;  // a capture failed on this lease: launch step by step from then on
+  // Every run ends with a kernel that copies the status word to host_status and clears it, so
+  // the next run on this lease starts from a clear word. Until a run has completed that way (a
+  // new lease, a failed launch or execution) the next run clears the word first.
+  bool status_clear = false;
+};
+
 struct Program {
   uint32_t magic = kProgramMagic;
   Context* ctx = nullptr;
+  // ---- immutable after create: shared by every run ----
   std::vector<SlotRecord> slots;
   std::vector<Step> steps;
   uint32_t n_inputs = 0, n_outputs = 0;
-  void* arena = nullptr;
-  uint64_t arena_bytes = 0;
-  std::vector<uint64_t> internal_offset;  // per slot (internal only)
-  double* scratch = nullptr;              // reduction partials
-  uint32_t* status = nullptr;             // device status word (inside the arena)
-  std::mutex run_mutex;
-  // HIP-graph replay: the whole step sequence captured once per distinct set of bound pointers
+  uint64_t arena_bytes = 0;               // per lease
+  uint64_t scratch_off = 0, scratch_side_off = 0;
+  std::vector<uint64_t> internal_offset;  // per slot (internal only), within a lease's arena
+  // Two-stream schedule (plan_streams): step j runs on the context stream (0) or its side
+  // stream (1), first waiting for the events recorded after the steps in wait_for[j];
+  // record_after[j] marks steps other-stream steps depend on. side_steps == 0: one stream.
+  uint32_t side_steps = 0;
+  std::vector<uint8_t> stream_of, record_after;
+  std::vector<std::vector<uint32_t>> wait_for;
+  // ---- settings and the lease pool, guarded by `mutex` ----
+  std::mutex mutex;
+  std::condition_variable lease_freed;
   bool graphs = true;
-  std::map<std::vector<void*>, hipGraphExec_t> graph_cache;
-  std::vector<std::vector<void*>> graph_order;  // insertion order, for eviction
+  bool concurrent = false;  // the two-stream plan is active
   bool profiling = false;
   uint64_t profiled_runs = 0;
   std::vector<double> step_ms;
-  std::vector<hipEvent_t> events;
-  // Asynchronous runs (shk_hip_program_run_async): the run's status word lands in host_status
-  // (pinned, this program's own) and `done` marks its end; `pending` until waited for.
-  uint32_t* host_status = nullptr;
-  hipEvent_t done = nullptr;
-  bool pending = false;
-  // Every run ends with a kernel that copies the device status word into host_status and clears
-  // it, so the next run starts from a clear word without a fill of its own. Until a run has
-  // completed that way (a new program, a failed launch or execution) the next run clears the
-  // word first.
-  bool status_clear = false;
-  // Two-stream schedule (plan_streams): step j runs on the context stream (0) or its side
-  // stream (1, with scratch_side as its reduction scratch), first waiting for the events
-  // recorded after the steps in wait_for[j]; record_after[j] marks steps other-stream steps
-  // depend on. `concurrent` is false when every step stays on stream 0.
-  bool concurrent = false;
-  uint32_t side_steps = 0;  // steps the plan puts on stream 1 (0: single-stream plan)
-  double* scratch_side = nullptr;
-  std::vector<uint8_t> stream_of, record_after;
-  std::vector<std::vector<uint32_t>> wait_for;
-  std::vector<hipEvent_t> step_done;
-  hipEvent_t fork = nullptr, join = nullptr;
+  std::vector<Lease*> leases;  // every lease, in creation order
+  std::vector<Lease*> idle;    // leases no run holds
+  uint32_t max_leases = 4;
+  // Asynchronous runs (shk_hip_program_run_async) not yet waited for, oldest first; each keeps
+  // its lease until shk_hip_program_wait (or the program's next run) observes its completion.
+  std::vector<Lease*> pending;
 };
 
 template <typename T, uint32_t M>
@@ -580,8 +597,8 @@ struct Bound {
   T* get(int32_t s) const { return s < 0 ? nullptr : static_cast<T*>(ptr[s]); }
 };
 
-hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipStream_t stream,
-                        double* scratch) {
+hipError_t enqueue_step(const Step& st, const Bound& b, hipStream_t stream, double* scratch,
+                        uint32_t* status) {
   const StepRecord& r = st.rec;
   const int32_t* s = r.slot;
   const int64_t* a = r.iarg;
@@ -611,7 +628,7 @@ hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipSt
         u.lr = r.farg[0]; u.momentum = r.farg[1]; u.dampening = r.farg[2]; u.weight_decay = r.farg[3];
         u.beta1 = r.farg[4]; u.beta2 = r.farg[5]; u.eps = r.farg[6];
         u.completed_steps = b.get<const int64_t>(s[6]);
-        u.status = pr.status;
+        u.status = status;
       }
       return shk::launch_gemm(p, reinterpret_cast<float*>(scratch), stream);
     }
@@ -650,7 +667,7 @@ hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipSt
     case OP_CE_INDEX:
       return shk::launch_index_ce(b.get<const float>(s[0]), b.get<const void>(s[1]), (int)a[2],
                                   b.get<float>(s[2]), b.get<float>(s[3]), a[0], a[1], (int)a[3], a[4],
-                                  r.farg[0], scratch, pr.status, stream);
+                                  r.farg[0], scratch, status, stream);
     case OP_OPTIMIZER: {
       shk::OptParams p{};
       const OptEntry* e = reinterpret_cast<const OptEntry*>(st.payload.data());
@@ -669,11 +686,11 @@ hipError_t enqueue_step(const Program& pr, const Step& st, const Bound& b, hipSt
       p.lr = r.farg[0]; p.momentum = r.farg[1]; p.dampening = r.farg[2]; p.weight_decay = r.farg[3];
       p.beta1 = r.farg[4]; p.beta2 = r.farg[5]; p.eps = r.farg[6];
       p.completed_steps = b.get<const int64_t>(s[0]);
-      p.status = pr.status;
+      p.status = status;
       return shk::launch_optimizer(p, stream);
     }
     case OP_STEP_COMMIT:
-      return shk::launch_step_commit(b.get<int64_t>(s[0]), pr.status, stream);
+      return shk::launch_step_commit(b.get<int64_t>(s[0]), status, stream);
     case OP_FILL:
       return shk::launch_fill(b.get<float>(s[0]), a[0], r.farg[0], stream);
     case OP_COPY:
@@ -764,7 +781,7 @@ void plan_streams(Program* pr) {
   pr->stream_of.assign(n, 0);
   pr->record_after.assign(n, 0);
   pr->wait_for.assign(n, {});
-  pr->concurrent = false;
+  pr->side_steps = 0;
   if (!concurrency_enabled() || n < 2) return;
   std::vector<Access> acc(n);
   for (size_t j = 0; j < n; ++j) acc[j] = step_access(pr->steps[j]);
@@ -787,64 +804,119 @@ void plan_streams(Program* pr) {
       pr->wait_for[j].push_back((uint32_t)latest);
       pr->record_after[latest] = 1;
     }
-    if (sj == 1) {
-      pr->concurrent = true;
-      pr->side_steps++;
-    }
+    if (sj == 1) pr->side_steps++;
   }
 }
 
-// Enqueues every step, then the status publication (copy to host_status, clear): on stream s0
-// alone, or along the two-stream plan (fork from s0, per-dependency events, join back into s0).
-// Profiling runs use s0 alone so that the per-step events bracket exactly one step each.
-// A program whose last step is the step commit has it performed by the publication kernel: the
-// commit reads the status word, so every step that can flag it precedes it, and nothing follows.
-hipError_t enqueue_steps(Program& pr, const Bound& b, hipStream_t s0, bool profile) {
+// Enqueues every step of one run on lease `ls`, then the status publication (copy to
+// ls.host_status, clear): on stream s0 alone, or along the two-stream plan (fork from s0,
+// per-dependency events, join back into s0). Profiling runs use s0 alone so that the per-step
+// events bracket exactly one step each. A program whose last step is the step commit has it
+// performed by the publication kernel: the commit reads the status word, so every step that can
+// flag it precedes it, and nothing follows.
+hipError_t enqueue_steps(const Program& pr, Lease& ls, const Bound& b, hipStream_t s0,
+                         bool two_streams, bool profile) {
   hipError_t e = hipSuccess;
   const size_t n = pr.steps.size();
   int64_t* commit = nullptr;
   if (n > 0 && pr.steps[n - 1].rec.opcode == OP_STEP_COMMIT)
     commit = b.get<int64_t>(pr.steps[n - 1].rec.slot[0]);
   const size_t launched = commit != nullptr ? n - 1 : n;
-  if (!pr.concurrent || profile) {
+  if (!two_streams || profile) {
     for (size_t i = 0; i < n; ++i) {
-      if (profile && (e = hipEventRecord(pr.events[i], s0)) != hipSuccess) return e;
-      if (i < launched && (e = enqueue_step(pr, pr.steps[i], b, s0, pr.scratch)) != hipSuccess)
+      if (profile && (e = hipEventRecord(ls.events[i], s0)) != hipSuccess) return e;
+      if (i < launched &&
+          (e = enqueue_step(pr.steps[i], b, s0, ls.scratch, ls.status)) != hipSuccess)
         return e;
     }
-    if (profile && (e = hipEventRecord(pr.events[n], s0)) != hipSuccess) return e;
-    return shk::launch_status_publish(pr.status, pr.host_status, commit, s0);
+    if (profile && (e = hipEventRecord(ls.events[n], s0)) != hipSuccess) return e;
+    return shk::launch_status_publish(ls.status, ls.host_status, commit, s0);
   }
   hipStream_t s1 = pr.ctx->side_stream;
-  if ((e = hipEventRecord(pr.fork, s0)) != hipSuccess || (e = hipStreamWaitEvent(s1, pr.fork, 0)) != hipSuccess)
+  if ((e = hipEventRecord(ls.fork, s0)) != hipSuccess ||
+      (e = hipStreamWaitEvent(s1, ls.fork, 0)) != hipSuccess)
     return e;
   for (size_t j = 0; j < launched; ++j) {
     const bool side = pr.stream_of[j] != 0;
     hipStream_t st = side ? s1 : s0;
     for (uint32_t i : pr.wait_for[j])
-      if ((e = hipStreamWaitEvent(st, pr.step_done[i], 0)) != hipSuccess) return e;
-    if ((e = enqueue_step(pr, pr.steps[j], b, st, side ? pr.scratch_side : pr.scratch)) != hipSuccess)
+      if ((e = hipStreamWaitEvent(st, ls.step_done[i], 0)) != hipSuccess) return e;
+    if ((e = enqueue_step(pr.steps[j], b, st, side ? ls.scratch_side : ls.scratch,
+                          ls.status)) != hipSuccess)
       return e;
-    if (pr.record_after[j] && (e = hipEventRecord(pr.step_done[j], st)) != hipSuccess) return e;
+    if (pr.record_after[j] && (e = hipEventRecord(ls.step_done[j], st)) != hipSuccess) return e;
   }
-  if ((e = hipEventRecord(pr.join, s1)) != hipSuccess) return e;
-  if ((e = hipStreamWaitEvent(s0, pr.join, 0)) != hipSuccess) return e;
-  return shk::launch_status_publish(pr.status, pr.host_status, commit, s0);
+  if ((e = hipEventRecord(ls.join, s1)) != hipSuccess) return e;
+  if ((e = hipStreamWaitEvent(s0, ls.join, 0)) != hipSuccess) return e;
+  return shk::launch_status_publish(ls.status, ls.host_status, commit, s0);
 }
 
-int32_t finish_run_locked(Program* pr);
+void destroy_lease(Lease* ls) {
+  if (ls == nullptr) return;
+  for (auto& kv : ls->graph_cache) (void)hipGraphExecDestroy(kv.second);
+  for (hipEvent_t e : ls->events)
+    if (e != nullptr) (void)hipEventDestroy(e);
+  for (hipEvent_t e : ls->step_done)
+    if (e != nullptr) (void)hipEventDestroy(e);
+  if (ls->done != nullptr) (void)hipEventDestroy(ls->done);
+  if (ls->fork != nullptr) (void)hipEventDestroy(ls->fork);
+  if (ls->join != nullptr) (void)hipEventDestroy(ls->join);
+  if (ls->host_status != nullptr) (void)hipHostFree(ls->host_status);
+  if (ls->arena != nullptr) (void)hipFree(ls->arena);
+  delete ls;
+}
+
+// Allocates one lease of `pr` (the device current): the zeroed arena, the pinned status word
+// and the run's events. Returns the status and leaves *out null on failure.
+int32_t create_lease(const Program& pr, Lease** out) {
+  *out = nullptr;
+  Lease* ls = new Lease();
+  if (hipMalloc(&ls->arena, pr.arena_bytes) != hipSuccess) {
+    ls->arena = nullptr;
+    destroy_lease(ls);
+    return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "program arena of %llu bytes failed",
+                (unsigned long long)pr.arena_bytes);
+  }
+  // Internal slots start zeroed; a lease's later runs see what earlier runs on it left.
+  if (hipMemset(ls->arena, 0, pr.arena_bytes) != hipSuccess) {
+    destroy_lease(ls);
+    return fail(SHK_HIP_STATUS_DEVICE_ERROR, "arena initialisation failed");
+  }
+  if (hipHostMalloc((void**)&ls->host_status, 16, hipHostMallocDefault) != hipSuccess) {
+    ls->host_status = nullptr;
+    destroy_lease(ls);
+    return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "pinned status allocation failed");
+  }
+  bool ok = hipEventCreateWithFlags(&ls->done, hipEventDisableTiming) == hipSuccess;
+  if (!ok) ls->done = nullptr;
+  ls->status = static_cast<uint32_t*>(ls->arena);
+  ls->scratch = reinterpret_cast<double*>(static_cast<char*>(ls->arena) + pr.scratch_off);
+  if (ok && pr.side_steps > 0) {
+    ls->scratch_side = reinterpret_cast<double*>(static_cast<char*>(ls->arena) + pr.scratch_side_off);
+    ok = hipEventCreateWithFlags(&ls->fork, hipEventDisableTiming) == hipSuccess;
+    if (!ok) ls->fork = nullptr;
+    ok = ok && hipEventCreateWithFlags(&ls->join, hipEventDisableTiming) == hipSuccess;
+    if (!ok) ls->join = nullptr;
+    ls->step_done.assign(pr.steps.size(), nullptr);
+    for (size_t j = 0; ok && j < pr.steps.size(); ++j)
+      if (pr.record_after[j] &&
+          hipEventCreateWithFlags(&ls->step_done[j], hipEventDisableTiming) != hipSuccess) {
+        ls->step_done[j] = nullptr;
+        ok = false;
+      }
+  }
+  if (!ok) {
+    destroy_lease(ls);
+    return fail(SHK_HIP_STATUS_DEVICE_ERROR, "event creation failed");
+  }
+  *out = ls;
+  return SHK_HIP_STATUS_OK;
+}
 
 void destroy_program(Program* p) {
   if (p == nullptr) return;
-  for (auto& kv : p->graph_cache) (void)hipGraphExecDestroy(kv.second);
-  for (hipEvent_t e : p->events) (void)hipEventDestroy(e);
-  if (p->done != nullptr) (void)hipEventDestroy(p->done);
-  for (hipEvent_t e : p->step_done)
-    if (e != nullptr) (void)hipEventDestroy(e);
-  if (p->fork != nullptr) (void)hipEventDestroy(p->fork);
-  if (p->join != nullptr) (void)hipEventDestroy(p->join);
-  if (p->host_status != nullptr) (void)hipHostFree(p->host_status);
-  if (p->arena != nullptr) (void)hipFree(p->arena);
+  for (Lease* ls : p->leases) destroy_lease(ls);
+  p->leases.clear();
   p->magic = 0;
   Context* c = p->ctx;
   delete p;
@@ -1507,13 +1579,14 @@ int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_
       return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image has trailing bytes");
     }
 
-    // Arena: status word, reduction scratch, then 256-byte aligned internal slots.
+    // Lease arena layout: status word, reduction scratch (one per stream), then 256-byte
+    // aligned internal slots.
     uint64_t off = 256;
-    const uint64_t scratch_off = off;
+    pr->scratch_off = off;
     off += ((scratch_doubles * 8 + 255) / 256) * 256;
     plan_streams(pr);
-    const uint64_t scratch_side_off = off;  // the side stream's own reduction scratch
-    if (pr->concurrent) off += ((scratch_doubles * 8 + 255) / 256) * 256;
+    pr->scratch_side_off = off;
+    if (pr->side_steps > 0) off += ((scratch_doubles * 8 + 255) / 256) * 256;
     pr->internal_offset.assign(h.n_slots, 0);
     for (uint32_t i = 0; i < h.n_slots; ++i) {
       if (pr->slots[i].kind != SLOT_INTERNAL) continue;
@@ -1521,50 +1594,36 @@ int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_
       off += ((pr->slots[i].bytes + 255) / 256) * 256;
     }
     pr->arena_bytes = off;
-    if (hipSetDevice(c->device) != hipSuccess || hipMalloc(&pr->arena, off) != hipSuccess) {
-      pr->arena = nullptr;
-      destroy_program(pr);
-      return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "program arena of %llu bytes failed",
-                  (unsigned long long)off);
-    }
-    // Internal slots start zeroed (optimizer slots, accumulators).
-    if (hipMemset(pr->arena, 0, off) != hipSuccess) {
-      destroy_program(pr);
-      return fail(SHK_HIP_STATUS_DEVICE_ERROR, "arena initialisation failed");
-    }
-    if (hipHostMalloc((void**)&pr->host_status, 16, hipHostMallocDefault) != hipSuccess) {
-      pr->host_status = nullptr;
-      destroy_program(pr);
-      return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "pinned status allocation failed");
-    }
-    if (hipEventCreateWithFlags(&pr->done, hipEventDisableTiming) != hipSuccess) {
-      pr->done = nullptr;
-      destroy_program(pr);
-      return fail(SHK_HIP_STATUS_DEVICE_ERROR, "event creation failed");
-    }
-    pr->status = static_cast<uint32_t*>(pr->arena);
-    pr->scratch = reinterpret_cast<double*>(static_cast<char*>(pr->arena) + scratch_off);
+    pr->concurrent = pr->side_steps > 0;
     if (pr->concurrent) {
-      pr->scratch_side = reinterpret_cast<double*>(static_cast<char*>(pr->arena) + scratch_side_off);
-      bool ok = hipEventCreateWithFlags(&pr->fork, hipEventDisableTiming) == hipSuccess &&
-                hipEventCreateWithFlags(&pr->join, hipEventDisableTiming) == hipSuccess;
-      pr->step_done.assign(pr->steps.size(), nullptr);
-      for (size_t j = 0; ok && j < pr->steps.size(); ++j)
-        if (pr->record_after[j])
-          ok = hipEventCreateWithFlags(&pr->step_done[j], hipEventDisableTiming) == hipSuccess;
-      if (ok) {
-        std::lock_guard<std::mutex> lock(c->mutex);
-        if (c->side_stream == nullptr &&
-            hipStreamCreateWithFlags(&c->side_stream, hipStreamNonBlocking) != hipSuccess) {
-          c->side_stream = nullptr;
-          ok = false;
-        }
-      }
-      if (!ok) {
+      std::lock_guard<std::mutex> lock(c->mutex);
+      if (c->side_stream == nullptr &&
+          (hipSetDevice(c->device) != hipSuccess ||
+           hipStreamCreateWithFlags(&c->side_stream, hipStreamNonBlocking) != hipSuccess)) {
+        c->side_stream = nullptr;
         destroy_program(pr);
-        return fail(SHK_HIP_STATUS_NO_COMMAND_QUEUE, "side stream or event creation failed");
+        return fail(SHK_HIP_STATUS_NO_COMMAND_QUEUE, "side stream creation failed");
       }
     }
+    {
+      const char* e = getenv("SHK_HIP_MAX_LEASES");
+      const long v = e != nullptr ? strtol(e, nullptr, 10) : 0;
+      if (v >= 1 && v <= 64) pr->max_leases = (uint32_t)v;
+    }
+    // The first lease is allocated here, so that a program that runs one call at a time never
+    // allocates device memory in a run.
+    if (hipSetDevice(c->device) != hipSuccess) {
+      destroy_program(pr);
+      return fail(SHK_HIP_STATUS_DEVICE_ERROR, "hipSetDevice failed");
+    }
+    Lease* first = nullptr;
+    const int32_t ls = create_lease(*pr, &first);
+    if (ls != SHK_HIP_STATUS_OK) {
+      destroy_program(pr);
+      return ls;
+    }
+    pr->leases.push_back(first);
+    pr->idle.push_back(first);
     pr->step_ms.assign(h.n_steps, 0.0);
     {
       const char* g = getenv("SHK_HIP_GRAPHS");
@@ -1588,6 +1647,7 @@ int32_t shk_hip_program_release(void* program) {
     std::lock_guard<std::mutex> lock(pr->ctx->mutex);
     (void)hipSetDevice(pr->ctx->device);
     (void)hipStreamSynchronize(pr->ctx->stream);
+    if (pr->ctx->side_stream != nullptr) (void)hipStreamSynchronize(pr->ctx->side_stream);
   }
   destroy_program(pr);
   return SHK_HIP_STATUS_OK;
@@ -1600,75 +1660,12 @@ int32_t shk_hip_program_arena_bytes(void* program, uint64_t* out_bytes) {
   return SHK_HIP_STATUS_OK;
 }
 
-int32_t shk_hip_program_set_graph_mode(void* program, int32_t enabled) {
+int32_t shk_hip_program_lease_count(void* program, uint32_t* out_leases) {
   Program* pr = checked<Program, kProgramMagic>(program);
-  if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
-  std::lock_guard<std::mutex> lock(pr->run_mutex);
-  if (pr->pending) {  // a pending asynchronous run completes (and reports) first
-    const int32_t st = finish_run_locked(pr);
-    if (st != SHK_HIP_STATUS_OK) return st;
-  }
-  pr->graphs = enabled != 0;
-  return SHK_HIP_STATUS_OK;
-}
-
-int32_t shk_hip_program_set_concurrent(void* program, int32_t enabled) {
-  Program* pr = checked<Program, kProgramMagic>(program);
-  if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
-  std::lock_guard<std::mutex> lock(pr->run_mutex);
-  if (pr->pending) {
-    const int32_t st = finish_run_locked(pr);
-    if (st != SHK_HIP_STATUS_OK) return st;
-  }
-  // captured graphs embed the schedule; the graph cache key includes it, so both stay cached
-  pr->concurrent = enabled != 0 && pr->side_steps > 0;
-  return SHK_HIP_STATUS_OK;
-}
-
-int32_t shk_hip_program_side_steps(void* program, uint32_t* out_steps) {
-  Program* pr = checked<Program, kProgramMagic>(program);
-  if (pr == nullptr || out_steps == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid arguments");
-  *out_steps = pr->concurrent ? pr->side_steps : 0;
-  return SHK_HIP_STATUS_OK;
-}
-
-int32_t shk_hip_program_step_count(void* program, uint32_t* out_steps) {
-  Program* pr = checked<Program, kProgramMagic>(program);
-  if (pr == nullptr || out_steps == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid arguments");
-  *out_steps = (uint32_t)pr->steps.size();
-  return SHK_HIP_STATUS_OK;
-}
-
-int32_t shk_hip_program_set_profiling(void* program, int32_t enabled) {
-  Program* pr = checked<Program, kProgramMagic>(program);
-  if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
-  std::lock_guard<std::mutex> lock(pr->run_mutex);
-  if (pr->pending) {  // a pending asynchronous run completes (and reports) first
-    const int32_t st = finish_run_locked(pr);
-    if (st != SHK_HIP_STATUS_OK) return st;
-  }
-  if (enabled && pr->events.empty()) {
-    (void)hipSetDevice(pr->ctx->device);
-    pr->events.resize(pr->steps.size() + 1, nullptr);
-    for (auto& e : pr->events) HIP_TRY(hipEventCreate(&e));
-  }
-  pr->profiling = enabled != 0;
-  pr->profiled_runs = 0;
-  std::fill(pr->step_ms.begin(), pr->step_ms.end(), 0.0);
-  return SHK_HIP_STATUS_OK;
-}
-
-int32_t shk_hip_program_step_times(void* program, double* out_milliseconds, uint32_t capacity, uint64_t* out_runs) {
-  Program* pr = checked<Program, kProgramMagic>(program);
-  if (pr == nullptr || (out_milliseconds == nullptr && capacity != 0))
+  if (pr == nullptr || out_leases == nullptr)
     return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid arguments");
-  std::lock_guard<std::mutex> lock(pr->run_mutex);
-  if (pr->pending) {  // a pending asynchronous run completes (and reports) first
-    const int32_t st = finish_run_locked(pr);
-    if (st != SHK_HIP_STATUS_OK) return st;
-  }
-  for (uint32_t i = 0; i < capacity && i < pr->step_ms.size(); ++i) out_milliseconds[i] = pr->step_ms[i];
-  if (out_runs) *out_runs = pr->profiled_runs;
+  std::lock_guard<std::mutex> lock(pr->mutex);
+  *out_leases = (uint32_t)pr->leases.size();
   return SHK_HIP_STATUS_OK;
 }
 
@@ -1676,36 +1673,98 @@ int32_t shk_hip_program_step_times(void* program, double* out_milliseconds, uint
 
 namespace {
 
-// Waits for the program's pending run and maps its status word (caller holds run_mutex).
-int32_t finish_run_locked(Program* pr) {
-  if (!pr->pending) return SHK_HIP_STATUS_OK;
-  const hipError_t se = hipEventSynchronize(pr->done);
-  pr->pending = false;
+// Observes the completion of the run held on `ls` and maps its status word, then returns the
+// lease to the pool. The caller holds no lock. Accumulates the run's step times when it was
+// profiled.
+int32_t finish_lease(Program* pr, Lease* ls, bool profiled) {
+  const hipError_t se = hipEventSynchronize(ls->done);
+  int32_t status = SHK_HIP_STATUS_OK;
   if (se != hipSuccess) {
-    pr->status_clear = false;
-    return fail(SHK_HIP_STATUS_EXECUTION_FAILED, "program execution failed: %s", hipGetErrorName(se));
+    ls->status_clear = false;
+    status = fail(SHK_HIP_STATUS_EXECUTION_FAILED, "program execution failed: %s",
+                  hipGetErrorName(se));
+  } else {
+    const uint32_t st = *ls->host_status;
+    if (st & shk::DEV_INDEX_OUT_OF_BOUNDS)
+      status = fail(SHK_HIP_STATUS_INDEX_OUT_OF_BOUNDS, "index target out of bounds");
+    else if (st & shk::DEV_NOT_POSITIVE)
+      status = fail(SHK_HIP_STATUS_ARITHMETIC,
+                    "adaptive bias correction or denominator is not positive");
+    else if (st & shk::DEV_NON_FINITE)
+      status = fail(SHK_HIP_STATUS_ARITHMETIC, "optimizer intermediate or candidate is not finite");
   }
-  if (pr->profiling) {
-    for (size_t i = 0; i < pr->steps.size(); ++i) {
-      float ms = 0.f;
-      HIP_TRY(hipEventElapsedTime(&ms, pr->events[i], pr->events[i + 1]));
-      pr->step_ms[i] += ms;
-    }
+  std::vector<float> ms;
+  if (profiled && se == hipSuccess) {
+    ms.resize(pr->steps.size(), 0.f);
+    for (size_t i = 0; i < pr->steps.size(); ++i)
+      if (hipEventElapsedTime(&ms[i], ls->events[i], ls->events[i + 1]) != hipSuccess) ms[i] = 0.f;
+  }
+  std::lock_guard<std::mutex> lock(pr->mutex);
+  if (!ms.empty()) {
+    for (size_t i = 0; i < ms.size(); ++i) pr->step_ms[i] += ms[i];
     pr->profiled_runs++;
   }
-  const uint32_t st = *pr->host_status;
-  if (st & shk::DEV_INDEX_OUT_OF_BOUNDS)
-    return fail(SHK_HIP_STATUS_INDEX_OUT_OF_BOUNDS, "index target out of bounds");
-  if (st & shk::DEV_NOT_POSITIVE)
-    return fail(SHK_HIP_STATUS_ARITHMETIC, "adaptive bias correction or denominator is not positive");
-  if (st & shk::DEV_NON_FINITE)
-    return fail(SHK_HIP_STATUS_ARITHMETIC, "optimizer intermediate or candidate is not finite");
-  return SHK_HIP_STATUS_OK;
+  pr->idle.push_back(ls);
+  pr->lease_freed.notify_one();
+  return status;
 }
 
-// Binds, validates and enqueues one run on the context stream; synchronous runs then wait for it,
-// asynchronous ones return with it pending. A run of a program whose previous asynchronous run
-// is still pending first waits for that one and returns its failure, if any, without launching.
+// Completes every asynchronous run of the program not yet waited for, oldest first, and returns
+// the first failure among them. The caller holds pr->mutex (released while waiting).
+int32_t finish_pending_locked(Program* pr, std::unique_lock<std::mutex>& lock) {
+  int32_t first = SHK_HIP_STATUS_OK;
+  std::string first_msg;
+  while (!pr->pending.empty()) {
+    Lease* ls = pr->pending.front();
+    pr->pending.erase(pr->pending.begin());
+    const bool profiled = !ls->events.empty() && pr->profiling;
+    lock.unlock();
+    const int32_t st = finish_lease(pr, ls, profiled);
+    if (st != SHK_HIP_STATUS_OK && first == SHK_HIP_STATUS_OK) {
+      first = st;
+      first_msg = g_last_error;
+    }
+    lock.lock();
+  }
+  if (first != SHK_HIP_STATUS_OK) g_last_error = first_msg;
+  return first;
+}
+
+// Takes an idle lease, or creates one while fewer than max_leases exist, or waits for one to be
+// returned. The caller holds pr->mutex through `lock`.
+int32_t acquire_lease(Program* pr, std::unique_lock<std::mutex>& lock, Lease** out) {
+  *out = nullptr;
+  for (;;) {
+    if (!pr->idle.empty()) {
+      *out = pr->idle.back();
+      pr->idle.pop_back();
+      return SHK_HIP_STATUS_OK;
+    }
+    if (pr->leases.size() < pr->max_leases) {
+      // Under the context mutex: allocation and the synchronous arena clear must not run while
+      // another thread captures a run's HIP graph on the context stream (captures hold it).
+      std::lock_guard<std::mutex> ctx_lock(pr->ctx->mutex);
+      HIP_TRY(hipSetDevice(pr->ctx->device));
+      Lease* ls = nullptr;
+      const int32_t st = create_lease(*pr, &ls);
+      if (st != SHK_HIP_STATUS_OK) return st;
+      pr->leases.push_back(ls);
+      *out = ls;
+      return SHK_HIP_STATUS_OK;
+    }
+    pr->lease_freed.wait(lock);
+  }
+}
+
+void return_lease(Program* pr, Lease* ls) {
+  std::lock_guard<std::mutex> lock(pr->mutex);
+  pr->idle.push_back(ls);
+  pr->lease_freed.notify_one();
+}
+
+// Binds, validates and enqueues one run on a lease of its own; synchronous runs then wait for
+// it, asynchronous ones return with it pending. Asynchronous runs of the program not yet waited
+// for are completed first, and the first failure among them is returned without launching.
 int32_t run_program(void* program, uint32_t input_count, void* const* inputs, uint32_t output_count,
                     void* const* outputs, bool async) {
   Program* pr = checked<Program, kProgramMagic>(program);
@@ -1733,10 +1792,7 @@ int32_t run_program(void* program, uint32_t input_count, void* const* inputs, ui
     std::vector<std::pair<uintptr_t, uintptr_t>> all;
     for (size_t i = 0; i < pr->slots.size(); ++i) {
       const SlotRecord& s = pr->slots[i];
-      if (s.kind == SLOT_INTERNAL) {
-        b.ptr[i] = static_cast<char*>(pr->arena) + pr->internal_offset[i];
-        continue;
-      }
+      if (s.kind == SLOT_INTERNAL) continue;  // bound to the lease's arena below
       Buffer* buf = s.kind == SLOT_OUTPUT ? out[s.ext_index] : in[s.ext_index];
       if (buf->bytes < s.bytes)
         return fail(SHK_HIP_STATUS_INCOMPATIBLE_RESOURCE, "slot %zu needs %llu bytes, bound buffer has %llu", i,
@@ -1755,36 +1811,67 @@ int32_t run_program(void* program, uint32_t input_count, void* const* inputs, ui
         return fail(SHK_HIP_STATUS_INCOMPATIBLE_RESOURCE, "an output or in-place input aliases another binding");
     }
 
-    std::lock_guard<std::mutex> run_lock(pr->run_mutex);
-    if (pr->pending) {
-      const int32_t st = finish_run_locked(pr);
+    Lease* ls = nullptr;
+    bool graphs, two_streams, profile;
+    {
+      std::unique_lock<std::mutex> lock(pr->mutex);
+      const int32_t st = finish_pending_locked(pr, lock);
       if (st != SHK_HIP_STATUS_OK) return st;
+      const int32_t la = acquire_lease(pr, lock, &ls);
+      if (la != SHK_HIP_STATUS_OK) return la;
+      graphs = pr->graphs && ls->graphs_ok;
+      two_streams = pr->concurrent;
+      profile = pr->profiling;
     }
+    for (size_t i = 0; i < pr->slots.size(); ++i)
+      if (pr->slots[i].kind == SLOT_INTERNAL)
+        b.ptr[i] = static_cast<char*>(ls->arena) + pr->internal_offset[i];
+
     std::unique_lock<std::mutex> ctx_lock(pr->ctx->mutex);
-    HIP_TRY(hipSetDevice(pr->ctx->device));
+    auto give_back = [&](int32_t status) {
+      ctx_lock.unlock();
+      return_lease(pr, ls);
+      return status;
+    };
+    if (hipSetDevice(pr->ctx->device) != hipSuccess)
+      return give_back(fail(SHK_HIP_STATUS_DEVICE_ERROR, "hipSetDevice failed"));
+    if (profile && ls->events.empty()) {
+      ls->events.assign(pr->steps.size() + 1, nullptr);
+      for (auto& e : ls->events)
+        if (hipEventCreate(&e) != hipSuccess) {
+          e = nullptr;
+          for (auto& x : ls->events)
+            if (x != nullptr) (void)hipEventDestroy(x);
+          ls->events.clear();
+          return give_back(fail(SHK_HIP_STATUS_DEVICE_ERROR, "event creation failed"));
+        }
+    }
     hipStream_t stream = pr->ctx->stream;
     std::vector<Buffer*> bound(in);
     bound.insert(bound.end(), out.begin(), out.end());
-    for (Buffer* x : bound) HIP_TRY(order_after_upload(x, stream));  // staged uploads landed
-    if (!pr->status_clear) {
+    for (Buffer* x : bound)  // staged uploads landed
+      if (order_after_upload(x, stream) != hipSuccess)
+        return give_back(fail(SHK_HIP_STATUS_DEVICE_ERROR, "waiting for a staged upload failed"));
+    if (!ls->status_clear) {
       // not cleared by a completed run's publication; from here until this run completes, a
       // failure leaves it unknown again
-      HIP_TRY(shk::launch_fill_u32(pr->status, 4, 0u, stream));
+      if (shk::launch_fill_u32(ls->status, 4, 0u, stream) != hipSuccess)
+        return give_back(fail(SHK_HIP_STATUS_EXECUTION_FAILED, "status clear failed"));
     }
-    pr->status_clear = false;
+    ls->status_clear = false;
     bool launched = false;
-    if (pr->graphs && !pr->profiling) {
+    if (graphs && !profile) {
       // cache key: the bound pointers, then the schedule (one stream / two streams)
       std::vector<void*> key(b.ptr);
-      key.push_back(reinterpret_cast<void*>(static_cast<uintptr_t>(pr->concurrent ? 2 : 1)));
-      auto it = pr->graph_cache.find(key);
-      if (it == pr->graph_cache.end()) {
+      key.push_back(reinterpret_cast<void*>(static_cast<uintptr_t>(two_streams ? 2 : 1)));
+      auto it = ls->graph_cache.find(key);
+      if (it == ls->graph_cache.end()) {
         // capture: every step + the status publication (kernels only, no memset or copy node)
         hipGraph_t graph = nullptr;
         hipGraphExec_t exec = nullptr;
         bool ok = hipStreamBeginCapture(stream, hipStreamCaptureModeRelaxed) == hipSuccess;
         if (ok) {
-          const bool steps_ok = enqueue_steps(*pr, b, stream, false) == hipSuccess;
+          const bool steps_ok = enqueue_steps(*pr, *ls, b, stream, two_streams, false) == hipSuccess;
           const bool ended = hipStreamEndCapture(stream, &graph) == hipSuccess;
           ok = steps_ok && ended && graph != nullptr &&
                hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess;
@@ -1792,57 +1879,134 @@ int32_t run_program(void* program, uint32_t input_count, void* const* inputs, ui
         }
         (void)hipGetLastError();  // a failed capture falls back to direct launches
         if (ok) {
-          if (pr->graph_order.size() >= 8) {
-            auto old = pr->graph_cache.find(pr->graph_order.front());
-            if (old != pr->graph_cache.end()) {
+          if (ls->graph_order.size() >= 8) {
+            auto old = ls->graph_cache.find(ls->graph_order.front());
+            if (old != ls->graph_cache.end()) {
               (void)hipGraphExecDestroy(old->second);
-              pr->graph_cache.erase(old);
+              ls->graph_cache.erase(old);
             }
-            pr->graph_order.erase(pr->graph_order.begin());
+            ls->graph_order.erase(ls->graph_order.begin());
           }
-          it = pr->graph_cache.emplace(key, exec).first;
-          pr->graph_order.push_back(key);
+          it = ls->graph_cache.emplace(key, exec).first;
+          ls->graph_order.push_back(key);
         } else {
           if (exec != nullptr) (void)hipGraphExecDestroy(exec);
-          pr->graphs = false;
+          ls->graphs_ok = false;
         }
       }
-      if (it != pr->graph_cache.end()) {
-        HIP_TRY(hipGraphLaunch(it->second, stream));
+      if (it != ls->graph_cache.end()) {
+        if (hipGraphLaunch(it->second, stream) != hipSuccess)
+          return give_back(fail(SHK_HIP_STATUS_EXECUTION_FAILED, "graph launch failed"));
         launched = true;
       }
     }
     if (!launched) {
-      const hipError_t e = enqueue_steps(*pr, b, stream, pr->profiling);
+      const hipError_t e = enqueue_steps(*pr, *ls, b, stream, two_streams, profile);
       if (e != hipSuccess) {
         (void)hipStreamSynchronize(stream);
         if (pr->ctx->side_stream != nullptr) (void)hipStreamSynchronize(pr->ctx->side_stream);
-        return fail(SHK_HIP_STATUS_EXECUTION_FAILED, "step launch failed: %s", hipGetErrorName(e));
+        return give_back(fail(SHK_HIP_STATUS_EXECUTION_FAILED, "step launch failed: %s",
+                              hipGetErrorName(e)));
       }
     }
-    HIP_TRY(hipEventRecord(pr->done, stream));
-    pr->pending = true;
-    pr->status_clear = true;  // once `done` completes without error
+    if (hipEventRecord(ls->done, stream) != hipSuccess) {
+      (void)hipStreamSynchronize(stream);
+      return give_back(fail(SHK_HIP_STATUS_DEVICE_ERROR, "event record failed"));
+    }
+    ls->status_clear = true;  // once `done` completes without error
     if (async) {
       // a later staged upload into any bound buffer waits for this run (write-after-read)
       for (Buffer* x : bound) {
-        if (x->last_use == nullptr) HIP_TRY(hipEventCreateWithFlags(&x->last_use, hipEventDisableTiming));
-        HIP_TRY(hipEventRecord(x->last_use, stream));
+        if (x->last_use == nullptr &&
+            hipEventCreateWithFlags(&x->last_use, hipEventDisableTiming) != hipSuccess) {
+          x->last_use = nullptr;
+          (void)hipStreamSynchronize(stream);
+          return give_back(fail(SHK_HIP_STATUS_DEVICE_ERROR, "event creation failed"));
+        }
+        if (hipEventRecord(x->last_use, stream) != hipSuccess) {
+          (void)hipStreamSynchronize(stream);
+          return give_back(fail(SHK_HIP_STATUS_DEVICE_ERROR, "event record failed"));
+        }
         x->use_pending = true;
       }
+      ctx_lock.unlock();
+      std::lock_guard<std::mutex> lock(pr->mutex);
+      pr->pending.push_back(ls);
       return SHK_HIP_STATUS_OK;
     }
     ctx_lock.unlock();
-    return finish_run_locked(pr);
+    return finish_lease(pr, ls, profile);
   } catch (const std::bad_alloc&) {
     return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "host allocation failed");
   } catch (...) {
     return fail(SHK_HIP_STATUS_INTERNAL_ERROR, "unexpected exception");
   }
 }
+
+// Applies a settings change with every pending asynchronous run completed first.
+template <typename F>
+int32_t with_settings(void* program, F f) {
+  Program* pr = checked<Program, kProgramMagic>(program);
+  if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
+  std::unique_lock<std::mutex> lock(pr->mutex);
+  const int32_t st = finish_pending_locked(pr, lock);
+  if (st != SHK_HIP_STATUS_OK) return st;
+  return f(pr);
+}
 }  // namespace
 
 extern "C" {
+
+int32_t shk_hip_program_set_graph_mode(void* program, int32_t enabled) {
+  return with_settings(program, [&](Program* pr) {
+    pr->graphs = enabled != 0;
+    return (int32_t)SHK_HIP_STATUS_OK;
+  });
+}
+
+int32_t shk_hip_program_set_concurrent(void* program, int32_t enabled) {
+  // captured graphs embed the schedule; the graph cache key includes it, so both stay cached
+  return with_settings(program, [&](Program* pr) {
+    pr->concurrent = enabled != 0 && pr->side_steps > 0;
+    return (int32_t)SHK_HIP_STATUS_OK;
+  });
+}
+
+int32_t shk_hip_program_side_steps(void* program, uint32_t* out_steps) {
+  Program* pr = checked<Program, kProgramMagic>(program);
+  if (pr == nullptr || out_steps == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid arguments");
+  std::lock_guard<std::mutex> lock(pr->mutex);
+  *out_steps = pr->concurrent ? pr->side_steps : 0;
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_program_step_count(void* program, uint32_t* out_steps) {
+  Program* pr = checked<Program, kProgramMagic>(program);
+  if (pr == nullptr || out_steps == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid arguments");
+  *out_steps = (uint32_t)pr->steps.size();
+  return SHK_HIP_STATUS_OK;
+}
+
+int32_t shk_hip_program_set_profiling(void* program, int32_t enabled) {
+  return with_settings(program, [&](Program* pr) {
+    pr->profiling = enabled != 0;
+    pr->profiled_runs = 0;
+    std::fill(pr->step_ms.begin(), pr->step_ms.end(), 0.0);
+    return (int32_t)SHK_HIP_STATUS_OK;
+  });
+}
+
+int32_t shk_hip_program_step_times(void* program, double* out_milliseconds, uint32_t capacity,
+                                   uint64_t* out_runs) {
+  if (out_milliseconds == nullptr && capacity != 0)
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid arguments");
+  return with_settings(program, [&](Program* pr) {
+    for (uint32_t i = 0; i < capacity && i < pr->step_ms.size(); ++i)
+      out_milliseconds[i] = pr->step_ms[i];
+    if (out_runs) *out_runs = pr->profiled_runs;
+    return (int32_t)SHK_HIP_STATUS_OK;
+  });
+}
 
 int32_t shk_hip_program_run(void* program, uint32_t input_count, void* const* inputs,
                             uint32_t output_count, void* const* outputs) {
@@ -1855,11 +2019,7 @@ int32_t shk_hip_program_run_async(void* program, uint32_t input_count, void* con
 }
 
 int32_t shk_hip_program_wait(void* program) {
-  Program* pr = checked<Program, kProgramMagic>(program);
-  if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
-  std::lock_guard<std::mutex> run_lock(pr->run_mutex);
-  return finish_run_locked(pr);
+  return with_settings(program, [](Program*) { return (int32_t)SHK_HIP_STATUS_OK; });
 }
-
 
 }  // extern "C"

@@ -66,6 +66,7 @@ EXPORTED_SYMBOLS = (
     "shk_hip_program_set_concurrent",
     "shk_hip_program_side_steps",
     "shk_hip_program_arena_bytes",
+    "shk_hip_program_lease_count",
     "shk_hip_program_set_profiling",
     "shk_hip_program_step_times",
     "shk_hip_program_step_count",
@@ -154,6 +155,7 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
             "shk_hip_program_set_concurrent": (i32, [vp, i32]),
             "shk_hip_program_side_steps": (i32, [vp, ctypes.POINTER(u32)]),
             "shk_hip_program_arena_bytes": (i32, [vp, ctypes.POINTER(u64)]),
+            "shk_hip_program_lease_count": (i32, [vp, ctypes.POINTER(u32)]),
             "shk_hip_program_set_profiling": (i32, [vp, i32]),
             "shk_hip_program_step_times": (i32, [vp, ctypes.POINTER(ctypes.c_double), u32,
                                                  ctypes.POINTER(u64)]),
@@ -385,6 +387,12 @@ class HipProgram:
     def wait(self) -> None:
         """Completes the pending asynchronous run, raising its failure (`shk_hip_program_wait`)."""
         check(self.lib, self.lib.shk_hip_program_wait(self.handle))
+
+    def lease_count(self) -> int:
+        """Per-run leases (arena, status word, events, graphs) the program has created."""
+        v = ctypes.c_uint32()
+        check(self.lib, self.lib.shk_hip_program_lease_count(self.handle, ctypes.byref(v)))
+        return v.value
 
     def arena_bytes(self) -> int:
         v = ctypes.c_uint64()

@@ -274,6 +274,23 @@ def test_mse_closed_forms_and_exact_quotient():
     assert bits(oracle.mse_mean(q, np.zeros(3, np.float32))) == bits(f32_of_fraction(Fraction(1, 3)))
 
 
+def test_mse_exact_reduction_against_rationals_and_sequential_saturation():
+    """mse_mean_exact is the contract's exactly rounded mean of the binary32 squares (Fraction
+    arithmetic); the reference CPU kernels' sequential binary32 sum (mse_mean) saturates once
+    the running sum reaches 2^24 with unit squares: n = 2^24 + 2^20 ones give a running sum of
+    exactly 2^24, so its mean is 2^24 / n, while the exact mean is 1."""
+    rng = np.random.default_rng(8)
+    p = rng.standard_normal(1001).astype(np.float32)
+    t = rng.standard_normal(1001).astype(np.float32)
+    sq = [Fraction(float((a - b) * (a - b))) for a, b in zip(p, t)]  # binary32 products
+    want = f32_of_fraction(sum(sq, Fraction(0)) / len(sq))
+    assert bits(oracle.mse_mean_exact(p, t)) == bits(want)
+    n = 2**24 + 2**20
+    ones, zeros = np.ones(n, np.float32), np.zeros(n, np.float32)
+    assert oracle.mse_mean_exact(ones, zeros) == 1.0
+    assert bits(oracle.mse_mean(ones, zeros)) == bits(f32_of_fraction(Fraction(2**24, n)))
+
+
 def test_index_ce_against_float64_and_bounds():
     rng = np.random.default_rng(6)
     logits = (rng.standard_normal((50, 10)) * 3).astype(np.float32)
@@ -422,3 +439,17 @@ def test_float64_gemm_mode_tracks_the_oracle_gemm_over_steps():
                          gemm="float64")
     assert np.array_equal(m._mm(A, B), oracle.matmul(A, B))
     assert np.array_equal(m._mm(A.T.copy(), B, trans_a=True), oracle.matmul(A, B))
+
+
+@pytest.mark.parametrize("decoupled,decay", [(False, 0.0), (False, 0.01), (True, 0.1)])
+def test_adam_apply_is_the_tail_of_adam_stage(decoupled, decay):
+    """adam_apply from the moments adam_stage produced gives adam_stage's parameters bit for bit
+    (the same tail; adam_stage is pinned by the reference's multi-step Adam oracle)."""
+    rng = np.random.default_rng(3)
+    p, g, m = (rng.standard_normal(5000).astype(np.float32) for _ in range(3))
+    v = np.abs(rng.standard_normal(5000)).astype(np.float32)
+    kw = dict(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=decay, decoupled=decoupled)
+    for steps in (0, 1, 7, 500):
+        pc, mc, vc = oracle.adam_stage(p, g, m, v, completed_steps=steps, **kw)
+        got = oracle.adam_apply(p, mc, vc, completed_steps=steps, **kw)
+        assert np.array_equal(got.view(np.uint32), pc.view(np.uint32))

@@ -177,6 +177,20 @@ int32_t shk_hip_program_run(void* program, uint32_t input_count, void* const* in
 int32_t shk_hip_program_run_async(void* program, uint32_t input_count, void* const* inputs,
                                   uint32_t output_count, void* const* outputs);
 int32_t shk_hip_program_wait(void* program);
+/* shk_hip_program_run without device allocation. No counterpart in the reference: a HIP
+ * addition for callers that cannot allocate device memory (code under HIP-graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). The run's per-run device memory (status word,
+ * reduction scratch, internal slots: shk_hip_program_arena_bytes) lives in a file-scope device
+ * array of the library, one 64 MiB copy per device, held until the process ends; a program
+ * needing more is refused with UNSUPPORTED_SHAPE. The call acquires no lease, captures no HIP
+ * graph and creates no event or buffer: it clears the array with a kernel, launches the steps
+ * on the context stream (the one-stream order), waits, and maps the status word as
+ * shk_hip_program_run does. Pending asynchronous runs of the program are completed first.
+ * Calls through one context are serialized; calls through different contexts of one device
+ * share the array and race -- callers must not overlap them. Results equal shk_hip_program_run's
+ * on a fresh lease. */
+int32_t shk_hip_program_run_static(void* program, uint32_t input_count, void* const* inputs,
+                                   uint32_t output_count, void* const* outputs);
 /* Two-stream step schedule (HIP addition; on by default unless SHK_HIP_CONCURRENT=0 when the
  * program is created): at creation each step's slot reads and writes give its dependencies, and a
  * step that does not depend on the step at the tail of the context stream runs beside it on a

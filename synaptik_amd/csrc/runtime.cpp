@@ -27,6 +27,14 @@
 #include "../../include/synaptik_hip.h"
 #include "kernels.h"
 
+// Device memory of shk_hip_program_run_static, the entry point that allocates nothing: a run's
+// status word, reduction scratch and internal slots, laid out as a lease arena. Each device the
+// library runs on holds one copy of it until the process ends. Host code never uses this name
+// as an address (on the host it names a stand-in): the device address of each device's copy is
+// resolved once, at context creation, and kept in g_scratch_address.
+constexpr uint64_t kStaticScratchBytes = 64ull << 20;
+__device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -48,6 +56,28 @@ int32_t fail(int32_t status, const char* fmt, ...) {
       return fail(SHK_HIP_STATUS_DEVICE_ERROR, "%s failed: %s", #expr, hipGetErrorName(e_));  \
   } while (0)
 
+// Per device ordinal: the device address of `scratch` (null until resolved), and whether its
+// resolution was attempted; guarded by g_scratch_mutex.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kMaxDevices] = {};
+hipError_t g_scratch_error[kMaxDevices] = {};
+
+// Resolves this device's copy of `scratch` (the device current; once per device).
+void resolve_static_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_address[device] != nullptr) return;
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e == hipSuccess && ptr != nullptr) {
+    g_scratch_address[device] = ptr;
+  } else {
+    g_scratch_error[device] = e != hipSuccess ? e : hipErrorInvalidSymbol;
+    (void)hipGetLastError();
+  }
+}
+
 constexpr uint32_t kContextMagic = 0x43484B53u;  // "SKHC"
 constexpr uint32_t kBufferMagic = 0x42484B53u;
 constexpr uint32_t kProgramMagic = 0x50484B53u;
@@ -61,7 +91,9 @@ struct Context {
   uint32_t magic = kContextMagic;
   int device = 0;
   hipStream_t stream = nullptr;
-  uint32_t* host_status = nullptr;  // pinned
+  // pinned status word of shk_hip_program_run_static runs, which hold the context mutex for
+  // their whole duration
+  uint32_t* host_status = nullptr;
   // Device staging of canonical publications: a 256-byte status block, then the packed bytes.
   // Grown on demand, guarded by `mutex`, freed with the context.
   uint8_t* pub_staging = nullptr;
@@ -947,6 +979,7 @@ int32_t shk_hip_context_create(int32_t device_ordinal, void** out_context) {
     if (device_ordinal < 0 || device_ordinal >= count)
       return fail(SHK_HIP_STATUS_NO_DEVICE, "device ordinal %d outside [0,%d)", device_ordinal, count);
     HIP_TRY(hipSetDevice(device_ordinal));
+    resolve_static_scratch(device_ordinal);
     Context* c = new Context();
     c->device = device_ordinal;
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
@@ -1765,51 +1798,67 @@ void return_lease(Program* pr, Lease* ls) {
 // Binds, validates and enqueues one run on a lease of its own; synchronous runs then wait for
 // it, asynchronous ones return with it pending. Asynchronous runs of the program not yet waited
 // for are completed first, and the first failure among them is returned without launching.
-int32_t run_program(void* program, uint32_t input_count, void* const* inputs, uint32_t output_count,
-                    void* const* outputs, bool async) {
-  Program* pr = checked<Program, kProgramMagic>(program);
-  if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
+// Checks the caller's bindings of a run and fills the external slots of `b` (internal slots
+// stay null); `bound` receives every bound buffer. Sizes, contexts and aliasing are validated.
+int32_t bind_external(Program* pr, uint32_t input_count, void* const* inputs,
+                      uint32_t output_count, void* const* outputs, Bound* b,
+                      std::vector<Buffer*>* bound) {
   if (input_count != pr->n_inputs || output_count != pr->n_outputs)
     return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "program expects %u inputs and %u outputs, got %u and %u",
                 pr->n_inputs, pr->n_outputs, input_count, output_count);
   if ((input_count && inputs == nullptr) || (output_count && outputs == nullptr))
     return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "null binding array");
+  std::vector<Buffer*> in(input_count), out(output_count);
+  for (uint32_t i = 0; i < input_count; ++i) {
+    in[i] = checked<Buffer, kBufferMagic>(inputs[i]);
+    if (in[i] == nullptr || in[i]->ctx != pr->ctx)
+      return fail(SHK_HIP_STATUS_INCOMPATIBLE_RESOURCE, "input %u is not a buffer of this context", i);
+  }
+  for (uint32_t i = 0; i < output_count; ++i) {
+    out[i] = checked<Buffer, kBufferMagic>(outputs[i]);
+    if (out[i] == nullptr || out[i]->ctx != pr->ctx)
+      return fail(SHK_HIP_STATUS_INCOMPATIBLE_RESOURCE, "output %u is not a buffer of this context", i);
+  }
+  b->ptr.assign(pr->slots.size(), nullptr);
+  std::vector<std::pair<uintptr_t, uintptr_t>> written;  // [begin,end) of outputs and in-place inputs
+  std::vector<std::pair<uintptr_t, uintptr_t>> all;
+  for (size_t i = 0; i < pr->slots.size(); ++i) {
+    const SlotRecord& s = pr->slots[i];
+    if (s.kind == SLOT_INTERNAL) continue;  // bound to the run's arena by the caller
+    Buffer* buf = s.kind == SLOT_OUTPUT ? out[s.ext_index] : in[s.ext_index];
+    if (buf->bytes < s.bytes)
+      return fail(SHK_HIP_STATUS_INCOMPATIBLE_RESOURCE, "slot %zu needs %llu bytes, bound buffer has %llu", i,
+                  (unsigned long long)s.bytes, (unsigned long long)buf->bytes);
+    b->ptr[i] = buf->ptr;
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(buf->ptr), hi = lo + std::max<uint64_t>(s.bytes, 1);
+    if (s.kind != SLOT_INPUT) written.push_back({lo, hi});
+    all.push_back({lo, hi});
+  }
+  // A written buffer may not overlap any other bound buffer (Metal: synaptik_metal_foundation.m:10012-10020).
+  for (const auto& w : written) {
+    int overlaps = 0;
+    for (const auto& o : all)
+      if (o.first < w.second && w.first < o.second) ++overlaps;
+    if (overlaps > 1)
+      return fail(SHK_HIP_STATUS_INCOMPATIBLE_RESOURCE, "an output or in-place input aliases another binding");
+  }
+  bound->assign(in.begin(), in.end());
+  bound->insert(bound->end(), out.begin(), out.end());
+  return SHK_HIP_STATUS_OK;
+}
+
+// Binds, validates and enqueues one run on a lease of its own; synchronous runs then wait for
+// it, asynchronous ones return with it pending. Asynchronous runs of the program not yet waited
+// for are completed first, and the first failure among them is returned without launching.
+int32_t run_program(void* program, uint32_t input_count, void* const* inputs, uint32_t output_count,
+                    void* const* outputs, bool async) {
+  Program* pr = checked<Program, kProgramMagic>(program);
+  if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
   try {
-    std::vector<Buffer*> in(input_count), out(output_count);
-    for (uint32_t i = 0; i < input_count; ++i) {
-      in[i] = checked<Buffer, kBufferMagic>(inputs[i]);
-      if (in[i] == nullptr || in[i]->ctx != pr->ctx)
-        return fail(SHK_HIP_STATUS_INCOMPATIBLE_RESOURCE, "input %u is not a buffer of this context", i);
-    }
-    for (uint32_t i = 0; i < output_count; ++i) {
-      out[i] = checked<Buffer, kBufferMagic>(outputs[i]);
-      if (out[i] == nullptr || out[i]->ctx != pr->ctx)
-        return fail(SHK_HIP_STATUS_INCOMPATIBLE_RESOURCE, "output %u is not a buffer of this context", i);
-    }
     Bound b;
-    b.ptr.assign(pr->slots.size(), nullptr);
-    std::vector<std::pair<uintptr_t, uintptr_t>> written;  // [begin,end) of outputs and in-place inputs
-    std::vector<std::pair<uintptr_t, uintptr_t>> all;
-    for (size_t i = 0; i < pr->slots.size(); ++i) {
-      const SlotRecord& s = pr->slots[i];
-      if (s.kind == SLOT_INTERNAL) continue;  // bound to the lease's arena below
-      Buffer* buf = s.kind == SLOT_OUTPUT ? out[s.ext_index] : in[s.ext_index];
-      if (buf->bytes < s.bytes)
-        return fail(SHK_HIP_STATUS_INCOMPATIBLE_RESOURCE, "slot %zu needs %llu bytes, bound buffer has %llu", i,
-                    (unsigned long long)s.bytes, (unsigned long long)buf->bytes);
-      b.ptr[i] = buf->ptr;
-      const uintptr_t lo = reinterpret_cast<uintptr_t>(buf->ptr), hi = lo + std::max<uint64_t>(s.bytes, 1);
-      if (s.kind != SLOT_INPUT) written.push_back({lo, hi});
-      all.push_back({lo, hi});
-    }
-    // A written buffer may not overlap any other bound buffer (Metal: synaptik_metal_foundation.m:10012-10020).
-    for (const auto& w : written) {
-      int overlaps = 0;
-      for (const auto& o : all)
-        if (o.first < w.second && w.first < o.second) ++overlaps;
-      if (overlaps > 1)
-        return fail(SHK_HIP_STATUS_INCOMPATIBLE_RESOURCE, "an output or in-place input aliases another binding");
-    }
+    std::vector<Buffer*> bound;
+    const int32_t bs = bind_external(pr, input_count, inputs, output_count, outputs, &b, &bound);
+    if (bs != SHK_HIP_STATUS_OK) return bs;
 
     Lease* ls = nullptr;
     bool graphs, two_streams, profile;
@@ -1847,8 +1896,6 @@ int32_t run_program(void* program, uint32_t input_count, void* const* inputs, ui
         }
     }
     hipStream_t stream = pr->ctx->stream;
-    std::vector<Buffer*> bound(in);
-    bound.insert(bound.end(), out.begin(), out.end());
     for (Buffer* x : bound)  // staged uploads landed
       if (order_after_upload(x, stream) != hipSuccess)
         return give_back(fail(SHK_HIP_STATUS_DEVICE_ERROR, "waiting for a staged upload failed"));
@@ -1943,6 +1990,78 @@ int32_t run_program(void* program, uint32_t input_count, void* const* inputs, ui
   }
 }
 
+// The no-allocation run: the arena of the run (status word, reduction scratch, internal slots)
+// is this device's copy of `scratch`, cleared by a fill kernel first; the steps run on the
+// context stream alone, launched directly (no graph is captured or instantiated, no event is
+// created), and the run's status is published to the context's pinned word. The context mutex
+// is held from the first launch until the stream has drained, so runs through one context never
+// overlap; runs through two contexts of one device share the array and race.
+int32_t run_static(void* program, uint32_t input_count, void* const* inputs,
+                   uint32_t output_count, void* const* outputs) {
+  Program* pr = checked<Program, kProgramMagic>(program);
+  if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
+  if (pr->arena_bytes > kStaticScratchBytes)
+    return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE,
+                "the program needs %llu bytes of per-run device memory (status word, reduction "
+                "scratch and internal slots); shk_hip_program_run_static holds at most %llu",
+                (unsigned long long)pr->arena_bytes, (unsigned long long)kStaticScratchBytes);
+  const int device = pr->ctx->device;
+  void* base = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (device >= 0 && device < kMaxDevices) base = g_scratch_address[device];
+    if (base == nullptr)
+      return fail(SHK_HIP_STATUS_DEVICE_ERROR, "static scratch of device %d unavailable: %s", device,
+                  hipGetErrorName(device >= 0 && device < kMaxDevices ? g_scratch_error[device]
+                                                                      : hipErrorInvalidDevice));
+  }
+  try {
+    Bound b;
+    std::vector<Buffer*> bound;
+    const int32_t bs = bind_external(pr, input_count, inputs, output_count, outputs, &b, &bound);
+    if (bs != SHK_HIP_STATUS_OK) return bs;
+    {
+      std::unique_lock<std::mutex> lock(pr->mutex);
+      const int32_t st = finish_pending_locked(pr, lock);
+      if (st != SHK_HIP_STATUS_OK) return st;
+    }
+    char* arena = static_cast<char*>(base);
+    for (size_t i = 0; i < pr->slots.size(); ++i)
+      if (pr->slots[i].kind == SLOT_INTERNAL) b.ptr[i] = arena + pr->internal_offset[i];
+    Lease view;  // the lease-shaped view of the static arena (owns nothing)
+    view.arena = arena;
+    view.status = reinterpret_cast<uint32_t*>(arena);
+    view.scratch = reinterpret_cast<double*>(arena + pr->scratch_off);
+    view.host_status = pr->ctx->host_status;
+
+    std::lock_guard<std::mutex> ctx_lock(pr->ctx->mutex);
+    HIP_TRY(hipSetDevice(device));
+    hipStream_t stream = pr->ctx->stream;
+    for (Buffer* x : bound) HIP_TRY(order_after_upload(x, stream));  // staged uploads landed
+    // The array keeps the last run's contents: clear the status word, the scratch and the
+    // internal slots, so this run sees what a fresh lease would.
+    hipError_t e = shk::launch_fill_u32(view.status, (int64_t)(pr->arena_bytes / 4), 0u, stream);
+    if (e == hipSuccess) e = enqueue_steps(*pr, view, b, stream, false, false);
+    const hipError_t se = hipStreamSynchronize(stream);
+    if (e != hipSuccess)
+      return fail(SHK_HIP_STATUS_EXECUTION_FAILED, "step launch failed: %s", hipGetErrorName(e));
+    if (se != hipSuccess)
+      return fail(SHK_HIP_STATUS_EXECUTION_FAILED, "program execution failed: %s", hipGetErrorName(se));
+    const uint32_t st = *view.host_status;
+    if (st & shk::DEV_INDEX_OUT_OF_BOUNDS)
+      return fail(SHK_HIP_STATUS_INDEX_OUT_OF_BOUNDS, "index target out of bounds");
+    if (st & shk::DEV_NOT_POSITIVE)
+      return fail(SHK_HIP_STATUS_ARITHMETIC, "adaptive bias correction or denominator is not positive");
+    if (st & shk::DEV_NON_FINITE)
+      return fail(SHK_HIP_STATUS_ARITHMETIC, "optimizer intermediate or candidate is not finite");
+    return SHK_HIP_STATUS_OK;
+  } catch (const std::bad_alloc&) {
+    return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "host allocation failed");
+  } catch (...) {
+    return fail(SHK_HIP_STATUS_INTERNAL_ERROR, "unexpected exception");
+  }
+}
+
 // Applies a settings change with every pending asynchronous run completed first.
 template <typename F>
 int32_t with_settings(void* program, F f) {
@@ -2016,6 +2135,11 @@ int32_t shk_hip_program_run(void* program, uint32_t input_count, void* const* in
 int32_t shk_hip_program_run_async(void* program, uint32_t input_count, void* const* inputs,
                                   uint32_t output_count, void* const* outputs) {
   return run_program(program, input_count, inputs, output_count, outputs, true);
+}
+
+int32_t shk_hip_program_run_static(void* program, uint32_t input_count, void* const* inputs,
+                                   uint32_t output_count, void* const* outputs) {
+  return run_static(program, input_count, inputs, output_count, outputs);
 }
 
 int32_t shk_hip_program_wait(void* program) {

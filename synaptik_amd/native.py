@@ -67,6 +67,7 @@ EXPORTED_SYMBOLS = (
     "shk_hip_program_side_steps",
     "shk_hip_program_arena_bytes",
     "shk_hip_program_lease_count",
+    "shk_hip_program_run_static",
     "shk_hip_program_set_profiling",
     "shk_hip_program_step_times",
     "shk_hip_program_step_count",
@@ -156,6 +157,8 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
             "shk_hip_program_side_steps": (i32, [vp, ctypes.POINTER(u32)]),
             "shk_hip_program_arena_bytes": (i32, [vp, ctypes.POINTER(u64)]),
             "shk_hip_program_lease_count": (i32, [vp, ctypes.POINTER(u32)]),
+            "shk_hip_program_run_static": (i32, [vp, u32, ctypes.POINTER(vp), u32,
+                                                 ctypes.POINTER(vp)]),
             "shk_hip_program_set_profiling": (i32, [vp, i32]),
             "shk_hip_program_step_times": (i32, [vp, ctypes.POINTER(ctypes.c_double), u32,
                                                  ctypes.POINTER(u64)]),
@@ -367,6 +370,15 @@ class HipProgram:
         ins = (ctypes.c_void_p * max(1, len(inputs)))(*[b.handle.value for b in inputs])
         outs = (ctypes.c_void_p * max(1, len(outputs)))(*[b.handle.value for b in outputs])
         check(self.lib, self.lib.shk_hip_program_run(self.handle, len(inputs), ins, len(outputs), outs))
+
+    def run_static(self, inputs, outputs) -> None:
+        """One run whose per-run device memory is the library's static per-device array
+        (`shk_hip_program_run_static`): allocates nothing; programs needing more than its
+        64 MiB are refused."""
+        ins = (ctypes.c_void_p * max(1, len(inputs)))(*[b.handle.value for b in inputs])
+        outs = (ctypes.c_void_p * max(1, len(outputs)))(*[b.handle.value for b in outputs])
+        check(self.lib, self.lib.shk_hip_program_run_static(self.handle, len(inputs), ins,
+                                                            len(outputs), outs))
 
     def run_async(self, inputs, outputs) -> None:
         """Enqueues one run and returns (`shk_hip_program_run_async`); `wait` completes it."""

@@ -146,8 +146,16 @@ class MlpSpec:
 
 
 def init_parameters(spec: MlpSpec, seed: int, scheme: str):
-    """Seeded initial weights: 'xavier_uniform' (bound sqrt(6/(fan_in+fan_out))) or
-    'he_normal' (sigma sqrt(2/fan_in)); biases zero (ParameterInitializers.java:269-372)."""
+    """Seeded initial weights, biases zero.
+
+    'builder': what `Model.builder().seed(seed)` creates for this Linear chain -- Glorot-uniform
+    weights from one L64X128MixRandom per builder step (initializers.builder_parameters).
+    'xavier_uniform' (bound sqrt(6/(fan_in+fan_out))) and 'he_normal' (sigma sqrt(2/fan_in)) draw
+    the same distributions as ParameterInitializers.java:269-372 from numpy's generator instead,
+    for seeded synthetic inputs."""
+    if scheme == "builder":
+        from .initializers import builder_parameters
+        return builder_parameters(spec, seed)
     rng = np.random.default_rng(seed)
     Ws, bs = [], []
     for l in spec.layers:

@@ -114,3 +114,13 @@ def test_optimizer_configuration_validation_mirrors_reference():
         MlpSpec([Dense(3, 4), Dense(5, 2)])
     with pytest.raises(ValueError):
         Dense(3, 4, "gelu")
+
+
+def test_library_exports_the_host_initialization_symbols():
+    text = (ROOT / "include" / "synaptik_init.h").read_text()
+    names = sorted(set(re.findall(r"\b(shk_lxm_[a-z_0-9]+)\s*\(", text)))
+    assert names == ["shk_lxm_next_double", "shk_lxm_next_long", "shk_lxm_seed",
+                     "shk_lxm_uniform_f32", "shk_lxm_uniform_f64"]
+    lib = native.load_library()
+    for name in names:
+        assert hasattr(lib, name), name

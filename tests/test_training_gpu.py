@@ -26,7 +26,7 @@ def _c1_data():
 
 def test_c1_twenty_step_loss_trajectory(ctx):
     spec = MlpSpec.chain([16, 64, 1], hidden="tanh", loss="mse")
-    Ws, bs = init_parameters(spec, 0, "xavier_uniform")
+    Ws, bs = init_parameters(spec, 0, "builder")  # Model.builder().seed(0)
     x, y = _c1_data()
     ref = oracle.OracleMLP(Ws, bs, ["tanh", None], "mse", dict(kind="sgd", lr=0.01))
     sess = HipTrainingSession.open(ctx, spec, Ws, bs, Sgd(0.01), 256)

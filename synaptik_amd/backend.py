@@ -204,7 +204,9 @@ class HipPartitionPreparer:
     def __init__(self, provider: Optional[HipCapabilityProvider] = None):
         self.provider = provider or HipCapabilityProvider()
 
-    def analyze(self, part: Partition) -> BackendPartitionAnalysis:
+    def analyze(self, context) -> BackendPartitionAnalysis:
+        """context: a PrepareContext (engine.py) or directly its partition graph."""
+        part = context.graph if hasattr(context, "graph") else context
         lw = _Lowering(part, self.provider)
         pb, ins, outs = lw.lower()
         image = pb.image()
@@ -251,8 +253,10 @@ class HipPreparedExecutable:
         self.analysis = analysis
         self.part = analysis.partition
 
-    def bind(self, inputs: dict) -> BoundInvocation:
-        """inputs: value id -> HipBuffer (accepted representations are this context's buffers)."""
+    def bind(self, inputs: dict, outputs: Optional[list] = None) -> BoundInvocation:
+        """inputs: value id -> HipBuffer (accepted representations are this context's buffers);
+        outputs: the run's buffers for the published values in order (created per run by the
+        schedule's buffer creators), or None to create them here."""
         bufs = []
         for v in self.part.inputs:
             b = inputs.get(v)
@@ -261,7 +265,16 @@ class HipPreparedExecutable:
             if b.nbytes < self.part.values[v].count * (8 if self.part.values[v].dtype == "INT64" else 4):
                 raise ValueError(f"input {v} buffer is too small")
             bufs.append(b)
-        outs = [self.ctx.buffer(max(s.nbytes, 4)) for s in self.analysis.output_slots]
+        if outputs is None:
+            outs = [self.ctx.buffer(max(s.nbytes, 4)) for s in self.analysis.output_slots]
+        else:
+            outs = list(outputs)
+            if len(outs) != len(self.analysis.output_slots):
+                raise ValueError("one buffer per published value is required")
+            for b, s in zip(outs, self.analysis.output_slots):
+                if not isinstance(b, HipBuffer) or b.ctx is not self.ctx or b.nbytes < s.nbytes:
+                    raise ValueError("an output representation is not an adequate buffer of "
+                                     "this backend's context")
         return BoundInvocation(self, bufs, outs)
 
     def run_values(self, values: dict) -> dict:

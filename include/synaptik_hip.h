@@ -158,6 +158,12 @@ int32_t shk_hip_buffer_download_storage(void* buffer, uint32_t element_width, in
 int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_bytes,
                                void** out_program);
 int32_t shk_hip_program_release(void* program);
+/* Decodes and validates an image exactly as shk_hip_program_create does, without a context or a
+ * device, and writes the per-run arena bytes one lease of the program would take
+ * (shk_hip_program_arena_bytes) -- the Workspace requirement a preparer reports at analysis
+ * time. HIP addition; returns the status shk_hip_program_create would for a malformed image. */
+int32_t shk_hip_program_validate(const void* image, uint64_t image_bytes,
+                                 uint64_t* out_arena_bytes);
 /* Runs the program once: binds in[i] / out[i] to the image's input / output slots by index,
  * validates sizes and aliasing (INCOMPATIBLE_RESOURCE), enqueues every step, waits, and maps
  * the device status word (ARITHMETIC, INDEX_OUT_OF_BOUNDS). Replaces

@@ -35,7 +35,8 @@ from typing import Optional, Sequence
 
 import numpy as np
 
-from .native import HipBuffer, HipContext, HipProgram, storage_transfer_bytes
+from .native import (HipBuffer, HipContext, HipProgram, storage_transfer_bytes,
+                     validate_program_image)
 from .program import ProgramBuilder, Slot
 
 BACKEND_ID = "hip"
@@ -210,7 +211,7 @@ class HipPartitionPreparer:
         lw = _Lowering(part, self.provider)
         pb, ins, outs = lw.lower()
         image = pb.image()
-        internal = sum(((s.nbytes + 255) // 256) * 256 for s in pb.slots if s.kind == 0)
+        internal = validate_program_image(image)  # one run's lease arena, no device needed
         reqs = [PreparationResourceRequirement("Buffer", v, part.values[v].count * 4 if part.values[v].dtype != "INT64" else part.values[v].count * 8)
                 for v in part.outputs]
         reqs.append(PreparationResourceRequirement("Workspace", "arena", internal))
@@ -218,15 +219,19 @@ class HipPartitionPreparer:
 
 
 class HipPartitionFinalizer:
-    """BackendPartitionFinalizer: creates the device program; releases it if anything fails."""
+    """BackendPartitionFinalizer: creates the device program; releases it if anything fails.
+    With a trace producer set (HipBackendIntegration.set_trace_observer), every prepared
+    executable gets a trace unit and every bound run emits its plan, timing and outcome."""
 
     def __init__(self, ctx: HipContext):
         self.ctx = ctx
+        self.tracer = None
 
     def finalize_partition(self, analysis: BackendPartitionAnalysis) -> "HipPreparedExecutable":
         program = HipProgram(self.ctx, analysis.plan)
         try:
-            return HipPreparedExecutable(self.ctx, program, analysis)
+            unit = self.tracer.prepare_unit() if self.tracer is not None else None
+            return HipPreparedExecutable(self.ctx, program, analysis, unit)
         except Exception:
             program.close()
             raise
@@ -239,7 +244,17 @@ class BoundInvocation:
         self.exe, self.inputs, self.outputs = exe, inputs, outputs
 
     def execute(self) -> list:
-        self.exe.program.run(self.inputs, self.outputs)
+        exe = self.exe
+        if exe.trace_unit is None:
+            exe.program.run(self.inputs, self.outputs)
+        else:
+            from .trace import TracedRun
+            a = exe.analysis
+            TracedRun(exe.trace_unit.producer, exe.trace_unit, len(self.inputs),
+                      len(self.outputs), sum(1 for r in a.requirements if r.kind == "Workspace"),
+                      sum(b.nbytes for b in self.inputs), sum(s.nbytes for s in a.output_slots),
+                      sum(r.byte_size for r in a.requirements if r.kind == "Workspace"))(
+                lambda: exe.program.run(self.inputs, self.outputs))
         return self.outputs
 
 
@@ -247,11 +262,13 @@ class HipPreparedExecutable:
     """PreparedExecutable: immutable, shared across runs; per-run outputs come from fresh buffers
     (the run's representations), the internal arena is owned by the program resource."""
 
-    def __init__(self, ctx: HipContext, program: HipProgram, analysis: BackendPartitionAnalysis):
+    def __init__(self, ctx: HipContext, program: HipProgram, analysis: BackendPartitionAnalysis,
+                 trace_unit=None):
         self.ctx = ctx
         self.program = program
         self.analysis = analysis
         self.part = analysis.partition
+        self.trace_unit = trace_unit
 
     def bind(self, inputs: dict, outputs: Optional[list] = None) -> BoundInvocation:
         """inputs: value id -> HipBuffer (accepted representations are this context's buffers);
@@ -319,6 +336,13 @@ class HipBackendIntegration:
     @classmethod
     def open(cls, device: int = 0) -> "HipBackendIntegration":
         return cls(device)
+
+    def set_trace_observer(self, observer) -> None:
+        """Routes invocation trace records (synaptik_amd/trace.py) of executables prepared from
+        now on to observer(record); None stops tracing new preparations."""
+        from .trace import HipTraceProducer
+        self.finalizer.tracer = None if observer is None else HipTraceProducer(
+            observer, BACKEND_ID, int(self.context.device))
 
     def availability_snapshot(self) -> dict:
         info = self.context.device_info()

@@ -557,6 +557,7 @@ hipError_t launch_copy(const float* src, float* dst, int64_t n, hipStream_t s) {
 }
 
 int64_t colsum_partial_doubles(int64_t R, int64_t N) {
+  if (R <= 0 || N <= 0) return 0;
   const int64_t rows = colsum_rows_per_panel(R, N);
   return ((R + rows - 1) / rows) * N;
 }

@@ -314,8 +314,10 @@ struct Validator {
   // Requires that slot s holds at least `elems` elements of dtype dt.
   bool holds(int32_t s, int64_t elems, uint32_t dt, const char* role) {
     if (s < 0) return true;
-    if (elems < 0) {
-      err = fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: negative extent for %s", step, role);
+    uint64_t need;
+    if (elems < 0 || __builtin_mul_overflow((uint64_t)elems, dtype_size(dt), &need)) {
+      err = fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: extent of %s is negative or too large",
+                 step, role);
       return false;
     }
     if (slots[s].dtype != dt) {
@@ -323,7 +325,6 @@ struct Validator {
                  step, role, s, slots[s].dtype, dt);
       return false;
     }
-    const uint64_t need = (uint64_t)elems * dtype_size(dt);
     if (slots[s].bytes < need) {
       err = fail(SHK_HIP_STATUS_RANGE_OUT_OF_BOUNDS,
                  "step %zu: %s slot %d has %llu bytes, operand needs %llu", step, role, s,
@@ -343,10 +344,22 @@ struct Validator {
   }
 };
 
-// Extent (in elements) spanned by a row-major matrix view of `rows` x `cols` with leading dim ld.
+// Product of two extents, or -1 when either is negative or the product does not fit int64
+// (every extent product of an image goes through here: the image is untrusted input).
+int64_t prod(int64_t a, int64_t b) {
+  int64_t r;
+  if (a < 0 || b < 0 || __builtin_mul_overflow(a, b, &r)) return -1;
+  return r;
+}
+
+// Extent (in elements) spanned by a row-major matrix view of `rows` x `cols` with leading dim ld,
+// or -1 when it does not fit int64.
 int64_t span(int64_t rows, int64_t cols, int64_t ld) {
   if (rows <= 0 || cols <= 0) return 0;
-  return (rows - 1) * ld + cols;
+  int64_t r;
+  if (ld < 0 || __builtin_mul_overflow(rows - 1, ld, &r) || __builtin_add_overflow(r, cols, &r))
+    return -1;
+  return r;
 }
 
 // GEMM whose epilogue stages an optimizer update from the gradient it computes (payload: one
@@ -403,7 +416,7 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
       if (M < 0 || N < 0 || K < 0 || (tA != 0 && tA != 1) || (tB != 0 && tB != 1) || act < 0 ||
           act > 3 || (mode != 0 && mode != 1))
         return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid GEMM attributes", idx);
-      if (M > INT32_MAX / 2 || N > INT32_MAX / 2)
+      if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX)
         return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: GEMM extent too large", idx);
       const bool empty = M == 0 || N == 0;  // touches no memory
       if (!empty && ((K > 0 && (tA ? lda < std::max<int64_t>(M, 1) : lda < K)) ||
@@ -413,8 +426,10 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
       if (mode == 1 && s[4] < 0)
         return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: activation gradient needs aux", idx);
       if (!st.payload.empty()) {
-        need((uint64_t)((shk::gemm_workspace_floats(M, N, K, false) + 1) / 2));  // in doubles
-        return validate_gemm_update(v, idx, st);
+        const int32_t u = validate_gemm_update(v, idx, st);
+        if (u == SHK_HIP_STATUS_OK)
+          need((uint64_t)((shk::gemm_workspace_floats(M, N, K, false) + 1) / 2));  // in doubles
+        return u;
       }
       if (!v.slot_ok(s[0], false, "A") || !v.slot_ok(s[1], false, "B") || !v.slot_ok(s[2], false, "C") ||
           !v.slot_ok(s[3], true, "bias") || !v.slot_ok(s[4], true, "aux"))
@@ -448,7 +463,7 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
       if (R < 0 || C < 0 || kind < 0 || kind > 3 || R > INT32_MAX)
         return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid row reduction", idx);
       if (!v.slot_ok(s[0], false, "X") || !v.slot_ok(s[1], false, "out") ||
-          !v.holds(s[0], R * C, DT_F32, "X") || !v.holds(s[1], R, DT_F32, "out") ||
+          !v.holds(s[0], prod(R, C), DT_F32, "X") || !v.holds(s[1], R, DT_F32, "out") ||
           !v.writable(s[1], "out"))
         return v.err;
       return SHK_HIP_STATUS_OK;
@@ -474,13 +489,13 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
       for (int k = 0; k < shk::PW_MAX_INPUTS; ++k) {
         if (!v.slot_ok(s[k], true, "pointwise input")) return v.err;
         const int64_t mode = a[2 + k];
-        const int64_t ext = mode == 0 ? R * C : mode == 1 ? C : mode == 2 ? R : 1;
+        const int64_t ext = mode == 0 ? prod(R, C) : mode == 1 ? C : mode == 2 ? R : 1;
         if (mode < 0 || mode > 3)
           return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: bad broadcast mode", idx);
         if (!v.holds(s[k], ext, DT_F32, "pointwise input")) return v.err;
       }
       for (int o = 0; o < shk::PW_MAX_OUTPUTS; ++o) {
-        if (!v.slot_ok(s[6 + o], true, "pointwise output") || !v.holds(s[6 + o], R * C, DT_F32, "pointwise output") ||
+        if (!v.slot_ok(s[6 + o], true, "pointwise output") || !v.holds(s[6 + o], prod(R, C), DT_F32, "pointwise output") ||
             !v.writable(s[6 + o], "pointwise output"))
           return v.err;
       }
@@ -501,7 +516,7 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
       if (R < 0 || C < 0 || R > INT32_MAX)
         return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid softmax shape", idx);
       if (!v.slot_ok(s[0], false, "X") || !v.slot_ok(s[1], false, "Y") || !v.slot_ok(s[2], true, "lse") ||
-          !v.holds(s[0], R * C, DT_F32, "X") || !v.holds(s[1], R * C, DT_F32, "Y") ||
+          !v.holds(s[0], prod(R, C), DT_F32, "X") || !v.holds(s[1], prod(R, C), DT_F32, "Y") ||
           !v.holds(s[2], R, DT_F32, "lse") || !v.writable(s[1], "Y") || !v.writable(s[2], "lse"))
         return v.err;
       return SHK_HIP_STATUS_OK;
@@ -511,8 +526,8 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
       if (R < 0 || C < 0 || R > INT32_MAX)
         return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid softmax shape", idx);
       if (!v.slot_ok(s[0], false, "Y") || !v.slot_ok(s[1], false, "G") || !v.slot_ok(s[2], false, "dX") ||
-          !v.slot_ok(s[3], true, "rowscale") || !v.holds(s[0], R * C, DT_F32, "Y") ||
-          !v.holds(s[1], R * C, DT_F32, "G") || !v.holds(s[2], R * C, DT_F32, "dX") ||
+          !v.slot_ok(s[3], true, "rowscale") || !v.holds(s[0], prod(R, C), DT_F32, "Y") ||
+          !v.holds(s[1], prod(R, C), DT_F32, "G") || !v.holds(s[2], prod(R, C), DT_F32, "dX") ||
           !v.holds(s[3], R, DT_F32, "rowscale") || !v.writable(s[2], "dX"))
         return v.err;
       return SHK_HIP_STATUS_OK;
@@ -521,9 +536,9 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
       const int64_t R = a[0], C = a[1];
       if (R < 0 || C < 0) return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid LSE shape", idx);
       if (!v.slot_ok(s[0], false, "X") || !v.slot_ok(s[1], false, "lse") || !v.slot_ok(s[2], true, "g") ||
-          !v.slot_ok(s[3], false, "dX") || !v.holds(s[0], R * C, DT_F32, "X") ||
+          !v.slot_ok(s[3], false, "dX") || !v.holds(s[0], prod(R, C), DT_F32, "X") ||
           !v.holds(s[1], R, DT_F32, "lse") || !v.holds(s[2], R, DT_F32, "g") ||
-          !v.holds(s[3], R * C, DT_F32, "dX") || !v.writable(s[3], "dX"))
+          !v.holds(s[3], prod(R, C), DT_F32, "dX") || !v.writable(s[3], "dX"))
         return v.err;
       return SHK_HIP_STATUS_OK;
     }
@@ -545,8 +560,8 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
         return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid cross-entropy shape", idx);
       if (!v.slot_ok(s[0], false, "logits") || !v.slot_ok(s[1], false, "target") ||
           !v.slot_ok(s[2], false, "loss") || !v.slot_ok(s[3], true, "grad") ||
-          !v.holds(s[0], R * C, DT_F32, "logits") || !v.holds(s[1], R, is64 ? DT_I64 : DT_I32, "target") ||
-          !v.holds(s[2], 1, DT_F32, "loss") || !v.holds(s[3], R * C, DT_F32, "grad") ||
+          !v.holds(s[0], prod(R, C), DT_F32, "logits") || !v.holds(s[1], R, is64 ? DT_I64 : DT_I32, "target") ||
+          !v.holds(s[2], 1, DT_F32, "loss") || !v.holds(s[3], prod(R, C), DT_F32, "grad") ||
           !v.writable(s[2], "loss") || !v.writable(s[3], "grad"))
         return v.err;
       need((uint64_t)shk::index_ce_partial_doubles(R));
@@ -613,7 +628,7 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
       if (a[0] < 0 || a[1] < 0 || a[0] > INT32_MAX / 2 || a[1] > INT32_MAX / 2)
         return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid transpose", idx);
       if (!v.slot_ok(s[0], false, "X") || !v.slot_ok(s[1], false, "Y") ||
-          !v.holds(s[0], a[0] * a[1], DT_F32, "X") || !v.holds(s[1], a[0] * a[1], DT_F32, "Y") ||
+          !v.holds(s[0], prod(a[0], a[1]), DT_F32, "X") || !v.holds(s[1], prod(a[0], a[1]), DT_F32, "Y") ||
           !v.writable(s[1], "Y"))
         return v.err;
       return SHK_HIP_STATUS_OK;
@@ -1530,6 +1545,103 @@ int32_t shk_hip_buffer_device_pointer(void* buffer, void** out_pointer) {
   return SHK_HIP_STATUS_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Decodes and validates a program image into `pr` (slots, steps, the stream plan and the lease
+// arena layout) without touching a device. Every step's operand extents are checked against its
+// slots' byte sizes, dtypes and writability, so no launch of a created program can address
+// outside a bound buffer.
+int32_t decode_image(const void* image, uint64_t image_bytes, Program* pr) {
+  const uint8_t* p = static_cast<const uint8_t*>(image);
+  const uint8_t* end = p + image_bytes;
+  if (image_bytes < sizeof(ImageHeader))
+    return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image shorter than its header");
+  ImageHeader h;
+  memcpy(&h, p, sizeof h);
+  p += sizeof h;
+  if (h.magic != kImageMagic || h.version != kImageVersion)
+    return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image magic/version mismatch");
+  if (h.n_slots > 1u << 20 || h.n_steps > 1u << 20 ||
+      (uint64_t)(end - p) < (uint64_t)h.n_slots * sizeof(SlotRecord))
+    return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image slot table truncated");
+  pr->slots.resize(h.n_slots);
+  memcpy(pr->slots.data(), p, h.n_slots * sizeof(SlotRecord));
+  p += h.n_slots * sizeof(SlotRecord);
+  std::vector<int> in_seen, out_seen;
+  for (uint32_t i = 0; i < h.n_slots; ++i) {
+    const SlotRecord& s = pr->slots[i];
+    if (dtype_size(s.dtype) == 0 || s.kind > SLOT_INOUT)
+      return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "slot %u has an invalid dtype or kind", i);
+    if (s.kind != SLOT_INTERNAL && s.ext_index >= h.n_slots)
+      return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "slot %u binding index out of range", i);
+    if (s.kind == SLOT_INPUT || s.kind == SLOT_INOUT) {
+      if (s.ext_index >= in_seen.size()) in_seen.resize(s.ext_index + 1, 0);
+      in_seen[s.ext_index]++;
+    } else if (s.kind == SLOT_OUTPUT) {
+      if (s.ext_index >= out_seen.size()) out_seen.resize(s.ext_index + 1, 0);
+      out_seen[s.ext_index]++;
+    }
+  }
+  for (size_t i = 0; i < in_seen.size(); ++i)
+    if (in_seen[i] != 1) {
+      return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "input index %zu bound %d times", i, in_seen[i]);
+    }
+  for (size_t i = 0; i < out_seen.size(); ++i)
+    if (out_seen[i] != 1) {
+      return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "output index %zu bound %d times", i, out_seen[i]);
+    }
+  pr->n_inputs = (uint32_t)in_seen.size();
+  pr->n_outputs = (uint32_t)out_seen.size();
+
+  uint64_t scratch_doubles = 0;
+  pr->steps.resize(h.n_steps);
+  for (uint32_t i = 0; i < h.n_steps; ++i) {
+    if ((uint64_t)(end - p) < sizeof(StepRecord)) {
+      return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image step %u truncated", i);
+    }
+    Step& st = pr->steps[i];
+    memcpy(&st.rec, p, sizeof(StepRecord));
+    p += sizeof(StepRecord);
+    const uint64_t padded = (st.rec.payload_bytes + 7u) & ~7ull;
+    if (st.rec.payload_bytes > 65536 || (uint64_t)(end - p) < padded) {
+      return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image step %u payload truncated", i);
+    }
+    st.payload.assign(p, p + st.rec.payload_bytes);
+    p += padded;
+    const int32_t v = validate_step(pr->slots, i, st, &scratch_doubles);
+    if (v != SHK_HIP_STATUS_OK) return v;
+  }
+  if (p != end) return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image has trailing bytes");
+
+  // Lease arena layout: status word, reduction scratch (one per stream), then 256-byte
+  // aligned internal slots.
+  constexpr uint64_t kMaxArena = 1ull << 50;  // far beyond any device; keeps the sums exact
+  if (scratch_doubles > kMaxArena / 8)
+    return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "reduction scratch too large");
+  uint64_t off = 256;
+  pr->scratch_off = off;
+  off += ((scratch_doubles * 8 + 255) / 256) * 256;
+  plan_streams(pr);
+  pr->scratch_side_off = off;
+  if (pr->side_steps > 0) off += ((scratch_doubles * 8 + 255) / 256) * 256;
+  pr->internal_offset.assign(h.n_slots, 0);
+  for (uint32_t i = 0; i < h.n_slots; ++i) {
+    if (pr->slots[i].kind != SLOT_INTERNAL) continue;
+    if (pr->slots[i].bytes > kMaxArena || off > kMaxArena)
+      return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "internal slot %u too large", i);
+    pr->internal_offset[i] = off;
+    off += ((pr->slots[i].bytes + 255) / 256) * 256;
+  }
+  pr->arena_bytes = off;
+  return SHK_HIP_STATUS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_bytes, void** out_program) {
   if (out_program == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "out_program is null");
   *out_program = nullptr;
@@ -1538,95 +1650,14 @@ int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_
     return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "invalid program arguments");
   Program* pr = nullptr;
   try {
-    const uint8_t* p = static_cast<const uint8_t*>(image);
-    const uint8_t* end = p + image_bytes;
-    if (image_bytes < sizeof(ImageHeader))
-      return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image shorter than its header");
-    ImageHeader h;
-    memcpy(&h, p, sizeof h);
-    p += sizeof h;
-    if (h.magic != kImageMagic || h.version != kImageVersion)
-      return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image magic/version mismatch");
-    if (h.n_slots > 1u << 20 || h.n_steps > 1u << 20 ||
-        (uint64_t)(end - p) < (uint64_t)h.n_slots * sizeof(SlotRecord))
-      return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image slot table truncated");
     pr = new Program();
     pr->ctx = c;
     c->refs.fetch_add(1);
-    pr->slots.resize(h.n_slots);
-    memcpy(pr->slots.data(), p, h.n_slots * sizeof(SlotRecord));
-    p += h.n_slots * sizeof(SlotRecord);
-    std::vector<int> in_seen, out_seen;
-    for (uint32_t i = 0; i < h.n_slots; ++i) {
-      const SlotRecord& s = pr->slots[i];
-      if (dtype_size(s.dtype) == 0 || s.kind > SLOT_INOUT) {
-        destroy_program(pr);
-        return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "slot %u has an invalid dtype or kind", i);
-      }
-      if (s.kind == SLOT_INPUT || s.kind == SLOT_INOUT) {
-        if (s.ext_index >= in_seen.size()) in_seen.resize(s.ext_index + 1, 0);
-        in_seen[s.ext_index]++;
-      } else if (s.kind == SLOT_OUTPUT) {
-        if (s.ext_index >= out_seen.size()) out_seen.resize(s.ext_index + 1, 0);
-        out_seen[s.ext_index]++;
-      }
-    }
-    for (size_t i = 0; i < in_seen.size(); ++i)
-      if (in_seen[i] != 1) {
-        destroy_program(pr);
-        return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "input index %zu bound %d times", i, in_seen[i]);
-      }
-    for (size_t i = 0; i < out_seen.size(); ++i)
-      if (out_seen[i] != 1) {
-        destroy_program(pr);
-        return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "output index %zu bound %d times", i, out_seen[i]);
-      }
-    pr->n_inputs = (uint32_t)in_seen.size();
-    pr->n_outputs = (uint32_t)out_seen.size();
-
-    uint64_t scratch_doubles = 0;
-    pr->steps.resize(h.n_steps);
-    for (uint32_t i = 0; i < h.n_steps; ++i) {
-      if ((uint64_t)(end - p) < sizeof(StepRecord)) {
-        destroy_program(pr);
-        return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image step %u truncated", i);
-      }
-      Step& st = pr->steps[i];
-      memcpy(&st.rec, p, sizeof(StepRecord));
-      p += sizeof(StepRecord);
-      const uint64_t padded = (st.rec.payload_bytes + 7u) & ~7ull;
-      if (st.rec.payload_bytes > 65536 || (uint64_t)(end - p) < padded) {
-        destroy_program(pr);
-        return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image step %u payload truncated", i);
-      }
-      st.payload.assign(p, p + st.rec.payload_bytes);
-      p += padded;
-      const int32_t v = validate_step(pr->slots, i, st, &scratch_doubles);
-      if (v != SHK_HIP_STATUS_OK) {
-        destroy_program(pr);
-        return v;
-      }
-    }
-    if (p != end) {
+    const int32_t ds = decode_image(image, image_bytes, pr);
+    if (ds != SHK_HIP_STATUS_OK) {
       destroy_program(pr);
-      return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "image has trailing bytes");
+      return ds;
     }
-
-    // Lease arena layout: status word, reduction scratch (one per stream), then 256-byte
-    // aligned internal slots.
-    uint64_t off = 256;
-    pr->scratch_off = off;
-    off += ((scratch_doubles * 8 + 255) / 256) * 256;
-    plan_streams(pr);
-    pr->scratch_side_off = off;
-    if (pr->side_steps > 0) off += ((scratch_doubles * 8 + 255) / 256) * 256;
-    pr->internal_offset.assign(h.n_slots, 0);
-    for (uint32_t i = 0; i < h.n_slots; ++i) {
-      if (pr->slots[i].kind != SLOT_INTERNAL) continue;
-      pr->internal_offset[i] = off;
-      off += ((pr->slots[i].bytes + 255) / 256) * 256;
-    }
-    pr->arena_bytes = off;
     pr->concurrent = pr->side_steps > 0;
     if (pr->concurrent) {
       std::lock_guard<std::mutex> lock(c->mutex);
@@ -1657,7 +1688,7 @@ int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_
     }
     pr->leases.push_back(first);
     pr->idle.push_back(first);
-    pr->step_ms.assign(h.n_steps, 0.0);
+    pr->step_ms.assign(pr->steps.size(), 0.0);
     {
       const char* g = getenv("SHK_HIP_GRAPHS");
       pr->graphs = !(g != nullptr && g[0] == '0');
@@ -1669,6 +1700,23 @@ int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_
     return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "host allocation failed");
   } catch (...) {
     destroy_program(pr);
+    return fail(SHK_HIP_STATUS_INTERNAL_ERROR, "unexpected exception");
+  }
+}
+
+int32_t shk_hip_program_validate(const void* image, uint64_t image_bytes,
+                                 uint64_t* out_arena_bytes) {
+  if (out_arena_bytes != nullptr) *out_arena_bytes = 0;
+  if (image == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "image is null");
+  try {
+    Program pr;  // decoded and discarded; no context, no device
+    const int32_t st = decode_image(image, image_bytes, &pr);
+    if (st == SHK_HIP_STATUS_OK && out_arena_bytes != nullptr) *out_arena_bytes = pr.arena_bytes;
+    pr.magic = 0;
+    return st;
+  } catch (const std::bad_alloc&) {
+    return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "host allocation failed");
+  } catch (...) {
     return fail(SHK_HIP_STATUS_INTERNAL_ERROR, "unexpected exception");
   }
 }

@@ -68,6 +68,7 @@ EXPORTED_SYMBOLS = (
     "shk_hip_program_arena_bytes",
     "shk_hip_program_lease_count",
     "shk_hip_program_run_static",
+    "shk_hip_program_validate",
     "shk_hip_program_set_profiling",
     "shk_hip_program_step_times",
     "shk_hip_program_step_count",
@@ -157,6 +158,7 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
             "shk_hip_program_side_steps": (i32, [vp, ctypes.POINTER(u32)]),
             "shk_hip_program_arena_bytes": (i32, [vp, ctypes.POINTER(u64)]),
             "shk_hip_program_lease_count": (i32, [vp, ctypes.POINTER(u32)]),
+            "shk_hip_program_validate": (i32, [vp, u64, ctypes.POINTER(u64)]),
             "shk_hip_program_run_static": (i32, [vp, u32, ctypes.POINTER(vp), u32,
                                                  ctypes.POINTER(vp)]),
             "shk_hip_program_set_profiling": (i32, [vp, i32]),
@@ -245,6 +247,16 @@ def _geometry(shape, strides):
     dims = (ctypes.c_int64 * max(1, rank))(*shape)
     st = None if strides is None else (ctypes.c_int64 * max(1, rank))(*[int(x) for x in strides])
     return dims, st, rank
+
+
+def validate_program_image(image: bytes) -> int:
+    """Decodes and validates a program image without a device (`shk_hip_program_validate`);
+    returns the per-run arena bytes of one lease, or raises the status program creation would."""
+    lib = load_library()
+    out = ctypes.c_uint64()
+    buf = ctypes.create_string_buffer(bytes(image), max(1, len(image)))
+    check(lib, lib.shk_hip_program_validate(buf, len(image), ctypes.byref(out)))
+    return out.value
 
 
 def storage_transfer_bytes(element_width: int, shape, strides, storage_offset: int) -> int:

@@ -111,3 +111,30 @@ def test_second_integration_with_the_same_id_is_rejected_and_closed():
     assert not first.context.handle
     with pytest.raises(RuntimeError):
         engine.prepare(mlp_train_partition(16, 8, 12, 4))
+
+
+def test_traced_invocations_report_outcomes():
+    """With a trace observer set, each bound run of a prepared executable emits its plan, timing
+    and outcome; an out-of-range label yields FAILED with the native status code."""
+    from synaptik_amd.trace import BackendInvocationOutcome, HipInvocationPlan, TraceOutcomeStatus
+    integ = HipBackendIntegration.open(0)
+    records = []
+    integ.set_trace_observer(records.append)
+    R, C = 64, 10
+    exe = integ.prepare(softmax_ce_partition(R, C))
+    rng = np.random.default_rng(0)
+    vals = {"x": rng.standard_normal((R, C)).astype(np.float32),
+            "g": rng.standard_normal((R, C)).astype(np.float32),
+            "labels": rng.integers(0, C, R).astype(np.int64)}
+    exe.run_values(vals)
+    bad = dict(vals, labels=np.full(R, C + 1, np.int64))
+    with pytest.raises(Exception):
+        exe.run_values(bad)
+    outcomes = [r for r in records if isinstance(r, BackendInvocationOutcome)]
+    plans = [r for r in records if isinstance(r, HipInvocationPlan)]
+    assert [o.status for o in outcomes] == [TraceOutcomeStatus.SUCCEEDED, TraceOutcomeStatus.FAILED]
+    assert outcomes[1].native_status.code == 16
+    assert plans[0].feed_slot_count == 3 and plans[0].aggregate_input_bytes == R * C * 8 + R * 8
+    assert plans[0].aggregate_internal_bytes > 0
+    exe.close()
+    integ.close()

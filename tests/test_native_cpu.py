@@ -124,3 +124,33 @@ def test_library_exports_the_host_initialization_symbols():
     lib = native.load_library()
     for name in names:
         assert hasattr(lib, name), name
+
+
+def test_image_validation_without_a_device():
+    """shk_hip_program_validate decodes an image as program creation does; it reports one run's
+    arena size, rejects hostile extents, and survives degenerate steps."""
+    from synaptik_amd.native import HipInvalidArgument, validate_program_image
+    pb = ProgramBuilder()
+    x, o = pb.input(5 * 4), pb.output(4)
+    t = pb.internal(1000)
+    pb.colsum(x, o, 5, 4)
+    pb.copy(x, t, 20)
+    arena = validate_program_image(pb.image())
+    assert arena >= 256 + 1000 * 4 and arena % 256 == 0
+    # a zero-width column sum once divided by zero while sizing its scratch
+    pb = ProgramBuilder()
+    x, o = pb.input(4), pb.output(1)
+    pb.colsum(x, o, 5, 0, ldx=1)
+    validate_program_image(pb.image())
+    # extents whose products overflow int64 must be refused, not wrap into a passing bound
+    for R, C, ld in ((2**40, 4, 2**30), (3, 2**62, 2**62)):
+        pb = ProgramBuilder()
+        x, o = pb.input(16), pb.output(16)
+        pb.colsum(x, o, R, C, ldx=ld)
+        with pytest.raises(HipInvalidArgument):
+            validate_program_image(pb.image())
+    pb = ProgramBuilder()
+    x, y = pb.input(16), pb.output(16)
+    pb.row_reduce(x, y, 2**31 - 1, 2**40, "sum")
+    with pytest.raises(HipInvalidArgument):
+        validate_program_image(pb.image())

@@ -46,7 +46,6 @@ struct V2Cfg {
   static constexpr int NI = BT / 32;      // copies per thread per operand per k-tile
   static constexpr int CPR = BT / 4;      // 16-byte chunks per k-row of an M/N-contiguous tile
   static constexpr int NG = NB * NB / 2;  // groups of 8 MFMAs per half k-tile
-  static constexpr int RPG = 4 * NB / NG;  // fragment reads (blocks) issued after a group
   static constexpr int CPG = 4 * NI / NG;  // copies issued after a group
   static constexpr int ECPR = WT / 4;     // 16-byte chunks per row of the epilogue transpose
 };
@@ -102,28 +101,65 @@ struct V2Loader {
 };
 
 // Fragments of one operand for one half (16 k) of a k-tile: f[b][s] is the value lane
-// (row 16b + lane % 16 of the wave's sub-tile; group g = lane / 16) supplies to MFMA s.
+// (MFMA row l16 = lane % 16 of block b; group g = lane / 16) supplies to MFMA s.
+//
+// K-contiguous operands: block b of the wave's sub-tile is rows 16b .. 16b + 15, and one
+// ds_read_b128 per block returns the four k values a lane needs (item b reads block b).
+// base[0] / base[1] are the offsets of this lane's chunk (4H + g) in the wave's rows 0..15 /
+// 16..31; blocks 2 and 3 repeat them 32 rows (1024 floats) further.
+//
+// M/N-contiguous operands are stored [k][row], where a 16-byte chunk holds four consecutive rows
+// at one k. Their blocks interleave instead: block b is the wave's rows NB r + b (r = 0..15), so
+// the NB values a lane needs at one k (row NB l16 + b of every block) are adjacent, and one read
+// of NB floats (ds_read_b128 for NB = 4, ds_read_b64 for NB = 2) per k fills f[0..NB)[s] (item s
+// reads MFMA step s). base[0] is the offset of (k = 4g, row NB l16); the k-row 16H + 4g + s
+// adds (16H + s) * BT (the chunk swizzle depends on (k / 4) mod 4 = g only). The epilogue maps
+// the accumulators back through the same interleave (v2_row / v2_col).
 template <bool KMAJ, int BT>
 struct V2Frag {
-  floatx4 f[V2Cfg<BT>::NB];
-  // K-contiguous: base[0] / base[1] are the offsets of this lane's chunk (4H + g) in the wave's
-  // rows 0..15 / 16..31; blocks 2 and 3 repeat them 32 rows (1024 floats) further.
-  // M/N-contiguous: base[b] is the offset of (k = 4g, row 16b + l16); the k-row 16H + 4g + s
-  // adds (16H + s) * BT (the swizzle depends on (k / 4) mod 4 = g only).
-  template <int H, int B>
-  __device__ __forceinline__ void load_block(const float* lds, const int* base) {
+  static constexpr int NB = V2Cfg<BT>::NB;
+  static constexpr int ITEMS = KMAJ ? NB : 4;  // fragment reads per half
+  floatx4 f[NB];
+  template <int H, int T>
+  __device__ __forceinline__ void load_item(const float* lds, const int* base) {
     if constexpr (KMAJ) {
-      f[B] = *reinterpret_cast<const floatx4*>(lds + base[B & 1] + (B >> 1) * 1024);
+      f[T] = *reinterpret_cast<const floatx4*>(lds + base[T & 1] + (T >> 1) * 1024);
+    } else if constexpr (NB == 4) {
+      const floatx4 v = *reinterpret_cast<const floatx4*>(lds + base[0] + (16 * H + T) * BT);
+      static_for<4>([&](auto b) { f[decltype(b)::value][T] = v[decltype(b)::value]; });
     } else {
-      static_for<4>([&](auto s) {
-        constexpr int S = decltype(s)::value;
-        f[B][S] = lds[base[B] + (16 * H + S) * BT];
-      });
+      typedef float floatx2 __attribute__((ext_vector_type(2)));
+      const floatx2 v = *reinterpret_cast<const floatx2*>(lds + base[0] + (16 * H + T) * BT);
+      f[0][T] = v[0];
+      f[1][T] = v[1];
     }
   }
   template <int H>
   __device__ __forceinline__ void load(const float* lds, const int* base) {
-    static_for<V2Cfg<BT>::NB>([&](auto b) { load_block<H, decltype(b)::value>(lds, base); });
+    static_for<ITEMS>([&](auto t) { load_item<H, decltype(t)::value>(lds, base); });
+  }
+};
+
+// Order in which the 2 NB-to-8 fragment reads of a half are issued: by the index of the first
+// MFMA that uses them (MFMA n = s NB^2 + i NB + j uses A item (KA ? i : s) and B item
+// (KB ? j : s)), A before B on ties; the all-K-contiguous case keeps A0 B0 B1 A1 B2 B3 A2 A3.
+template <bool KA, bool KB, int NB>
+struct V2ReadOrder {
+  static constexpr int IA = KA ? NB : 4, IB = KB ? NB : 4, N = IA + IB;
+  int op[8] = {}, idx[8] = {};
+  constexpr V2ReadOrder() {
+    if (KA && KB && NB == 4) {
+      const int o[8] = {0, 1, 1, 0, 1, 1, 0, 0}, b[8] = {0, 0, 1, 1, 2, 3, 2, 3};
+      for (int t = 0; t < 8; ++t) { op[t] = o[t]; idx[t] = b[t]; }
+      return;
+    }
+    int ia = 0, ib = 0;
+    for (int t = 0; t < N; ++t) {
+      const int ua = ia < IA ? (KA ? ia * NB : ia * NB * NB) : 1 << 20;
+      const int ub = ib < IB ? (KB ? ib : ib * NB * NB) : 1 << 20;
+      if (ua <= ub) { op[t] = 0; idx[t] = ia++; }
+      else { op[t] = 1; idx[t] = ib++; }
+    }
   }
 };
 
@@ -191,18 +227,21 @@ gemm_f32_v2(GemmParams p) {
   la.init(p.lda);
   lb.init(p.ldb);
 
-  // lane-dependent fragment offsets per half
+  // lane-dependent fragment offsets per half (see V2Frag)
   int a_base[2][NB], b_base[2][NB];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
       a_base[h][q] = KA ? v2_kmaj_off(wm * WT + 16 * (q & 1) + l16, 4 * h + g)
-                        : v2_mnmaj_off(4 * g, wm * WT + 16 * q + l16, Cfg::CPR);
+                        : v2_mnmaj_off(4 * g, wm * WT + NB * l16, Cfg::CPR);
       b_base[h][q] = KB ? v2_kmaj_off(wn * WT + 16 * (q & 1) + l16, 4 * h + g)
-                        : v2_mnmaj_off(4 * g, wn * WT + 16 * q + l16, Cfg::CPR);
+                        : v2_mnmaj_off(4 * g, wn * WT + NB * l16, Cfg::CPR);
     }
   }
+  // wave sub-tile row of accumulator register R of block I, column of block J (lane column l16)
+  auto v2_row = [&](int I, int R) { return KA ? 16 * I + 4 * g + R : NB * (4 * g + R) + I; };
+  auto v2_col = [&](int J) { return KB ? 16 * J + l16 : NB * l16 + J; };
 
   floatx4 acc[NB][NB];
   static_for<NB>([&](auto i) {
@@ -229,16 +268,17 @@ gemm_f32_v2(GemmParams p) {
       __builtin_amdgcn_sched_barrier(0);
     });
   };
-  // Fragment reads of half H from stage (As, Bs): read item t (t < 2 NB) in the order
-  // A0, B0, B1, A1, B2, B3, A2, A3, so that the blocks the next half's first MFMAs use come
-  // first; group q issues items q RPG .. q RPG + RPG - 1.
+  // Fragment reads of half H from stage (As, Bs): read item t in V2ReadOrder (the items the next
+  // half's first MFMAs use come first); group q issues items q RPG .. q RPG + RPG - 1.
+  constexpr V2ReadOrder<KA, KB, NB> kOrder{};
+  constexpr int NREAD = kOrder.N, RPG = (NREAD + NG / 2 - 1) / (NG / 2);
   auto read_item = [&](auto t, V2Frag<KA, BT>& fa, V2Frag<KB, BT>& fb, const float* As,
                        const float* Bs, auto h) {
     constexpr int T = decltype(t)::value, H = decltype(h)::value;
-    constexpr int ORDER_OP[8] = {0, 1, 1, 0, 1, 1, 0, 0};
-    constexpr int ORDER_BLK[8] = {0, 0, 1, 1, 2, 3, 2, 3};
-    if constexpr (ORDER_OP[T] == 0) fa.template load_block<H, ORDER_BLK[T]>(As, a_base[H]);
-    else fb.template load_block<H, ORDER_BLK[T]>(Bs, b_base[H]);
+    if constexpr (T < NREAD) {
+      if constexpr (kOrder.op[T] == 0) fa.template load_item<H, kOrder.idx[T]>(As, a_base[H]);
+      else fb.template load_item<H, kOrder.idx[T]>(Bs, b_base[H]);
+    }
   };
   // Copies of a k-tile: item c (c < 2 NI) is operand c % 2, instruction c / 2.
   auto copy_item = [&](auto c, const float* at, const float* bt, float* As, float* Bs, int k_left) {
@@ -293,8 +333,8 @@ gemm_f32_v2(GemmParams p) {
     mfma_half(fa0, fb0, [&](auto q) {
       constexpr int Q = decltype(q)::value;
       if constexpr (Q < NG / 2) {
-        static_for<Cfg::RPG>([&](auto r) {
-          read_item(std::integral_constant<int, Q * Cfg::RPG + decltype(r)::value>{}, fa1, fb1,
+        static_for<RPG>([&](auto r) {
+          read_item(std::integral_constant<int, Q * RPG + decltype(r)::value>{}, fa1, fb1,
                     Acur, Bcur, std::integral_constant<int, 1>{});
         });
       }
@@ -308,8 +348,8 @@ gemm_f32_v2(GemmParams p) {
       constexpr int Q = decltype(q)::value;
       if constexpr (Q < NG / 2) {
         if (more) {
-          static_for<Cfg::RPG>([&](auto r) {
-            read_item(std::integral_constant<int, Q * Cfg::RPG + decltype(r)::value>{}, fa0, fb0,
+          static_for<RPG>([&](auto r) {
+            read_item(std::integral_constant<int, Q * RPG + decltype(r)::value>{}, fa0, fb0,
                       Aoth, Both, std::integral_constant<int, 0>{});
           });
         }
@@ -336,17 +376,16 @@ gemm_f32_v2(GemmParams p) {
   // (row-major, 16-byte chunks XOR-swizzled by row) so that every global access of the epilogue
   // is a 16-byte row segment: lane (q = lane % ECPR, rg = lane / ECPR) owns columns 4q..4q+3 of
   // rows rg + (64 / ECPR) t, and each store instruction covers whole WT-float row segments.
-  const int64_t row_w = m0 + wm * WT + 4 * g, col_w = n0 + wn * WT + l16;
   if (p.partial != nullptr) {
     // split-K: raw partial sums, reduced (and given the epilogue) by gemm_splitk_reduce
     float* part = p.partial + (int64_t)blockIdx.y * p.M * p.N;
     static_for<NB>([&](auto i) {
       static_for<NB>([&](auto j) {
         constexpr int I = decltype(i)::value, J = decltype(j)::value;
-        const int64_t col = col_w + 16 * J;
+        const int64_t col = n0 + wn * WT + v2_col(J);
         static_for<4>([&](auto r) {
           constexpr int R = decltype(r)::value;
-          const int64_t row = row_w + 16 * I + R;
+          const int64_t row = m0 + wm * WT + v2_row(I, R);
           if (!TAIL || (row < p.M && col < p.N)) part[row * p.N + col] = acc[I][J][R];
         });
       });
@@ -389,16 +428,34 @@ gemm_f32_v2(GemmParams p) {
   const int arr = wave / PER_ARRAY;
   float* stage = (arr == 0 ? As0 : arr == 1 ? Bs0 : arr == 2 ? As1 : Bs1) +
                  (wave % PER_ARRAY) * (WT * WT);
-  static_for<NB>([&](auto i) {
-    static_for<NB>([&](auto j) {
-      constexpr int I = decltype(i)::value, J = decltype(j)::value;
-      static_for<4>([&](auto r) {
-        constexpr int R = decltype(r)::value;
-        const int row = 16 * I + 4 * g + R, col = 16 * J + l16;
-        stage[row * WT + (((col >> 2) ^ (row % ECPR)) << 2) + (col & 3)] = acc[I][J][R];
+  if constexpr (KB) {
+    static_for<NB>([&](auto i) {
+      static_for<NB>([&](auto j) {
+        constexpr int I = decltype(i)::value, J = decltype(j)::value;
+        static_for<4>([&](auto r) {
+          constexpr int R = decltype(r)::value;
+          const int row = v2_row(I, R), col = v2_col(J);
+          stage[row * WT + (((col >> 2) ^ (row % ECPR)) << 2) + (col & 3)] = acc[I][J][R];
+        });
       });
     });
-  });
+  } else {
+    // the NB columns NB l16 + J (J < NB) of a lane are adjacent: one NB-float store per row
+    static_for<NB>([&](auto i) {
+      static_for<4>([&](auto r) {
+        constexpr int I = decltype(i)::value, R = decltype(r)::value;
+        const int row = v2_row(I, R), col = NB * l16;
+        float* dst = stage + row * WT + (((col >> 2) ^ (row % ECPR)) << 2) + (col & 3);
+        if constexpr (NB == 4) {
+          *reinterpret_cast<floatx4*>(dst) =
+              floatx4{acc[I][0][R], acc[I][1][R], acc[I][2][R], acc[I][3][R]};
+        } else {
+          typedef float floatx2 __attribute__((ext_vector_type(2)));
+          *reinterpret_cast<floatx2*>(dst) = floatx2{acc[I][0][R], acc[I][1][R]};
+        }
+      });
+    });
+  }
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are complete
   const int q = lane % ECPR, rg = lane / ECPR;
   auto tile_row = [&](int t) -> floatx4 {

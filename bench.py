@@ -87,8 +87,9 @@ def cpu_baseline(sample_batch: int, seed=0) -> dict:
     return {
         "value": BATCH / step_s,
         "unit": "samples/s",
-        "cores": 1,
+        **host_cores(),
         "kind": "port",
+        "extrapolated": True,
         "sample": (f"oracle forward+backward of MLP-4096 on {sample_batch} of the 4096 rows "
                    f"({t_fb:.2f} s, scaled x{BATCH / sample_batch:.2f}) + one full SGD-momentum stage "
                    f"of all parameters ({t_upd:.2f} s): {step_s:.1f} s per 4096-sample step"),
@@ -130,6 +131,7 @@ def openblas_baseline(threads: int, sample_batch: int, seed=0) -> dict:
     step_s = (BATCH / sample_batch) * t_fb + t_upd
     version = next((i.get("version") for i in threadpool_info() if i["internal_api"] == "openblas"), None)
     return {"value": BATCH / step_s, "unit": "samples/s", "threads": threads,
+            "nproc": host_cores()["nproc"], "extrapolated": sample_batch < BATCH,
             "kind": "openblas route (numpy's OpenBLAS %s), not the reference's default route" % version,
             "sample": (f"{sample_batch} of the 4096 rows ({t_fb:.2f} s, scaled x{BATCH / sample_batch:.0f}) "
                        f"+ one full SGD update ({t_upd:.2f} s)")}
@@ -172,7 +174,7 @@ def secondary(ctx, reps: int = 5, cpu: bool = True) -> dict:
     """The other benchmark configurations, measured on the same context (not the headline value)."""
     from synaptik_amd.native import HipProgram
     from synaptik_amd.program import ProgramBuilder
-    from synaptik_amd.training import (Adam, HipTrainingSession, MlpSpec, init_parameters,
+    from synaptik_amd.training import (Adam, HipTrainingSession, MlpSpec, Sgd, init_parameters,
                                        lower_dense_layer)
     out = {}
     rng = np.random.default_rng(7)
@@ -252,6 +254,27 @@ def secondary(ctx, reps: int = 5, cpu: bool = True) -> dict:
                                  "objective_step1": first, "objective_step50": last,
                                  "timed": "steps 51-250"}
     sess.close()
+    # C1: 16 -> 64 -> 1 tanh MLP, MSE, SGD 0.01, batch 256 (builder weights, seed 0): the
+    # 20-step run, launch-bound; the first run also captures the step's graph
+    spec = MlpSpec.chain([16, 64, 1], hidden="tanh", loss="mse")
+    Ws, bs = init_parameters(spec, 0, "builder")
+    sess = HipTrainingSession.open(ctx, spec, Ws, bs, Sgd(0.01), 256)
+    x1 = ctx.upload(rng.standard_normal((256, 16)).astype(np.float32))
+    y1 = ctx.upload(rng.standard_normal((256, 1)).astype(np.float32))
+    t0 = time.perf_counter()
+    for _ in range(20):
+        sess.run_resident(x1, y1)
+    first = float(sess.objective())
+    cold = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for _ in range(20 * reps):
+        sess.run_resident(x1, y1)
+    float(sess.objective())
+    warm = (time.perf_counter() - t0) / reps
+    out["c1_plumbing_mlp"] = {"ms_20_steps": round(warm * 1e3, 3),
+                              "ms_20_steps_first": round(cold * 1e3, 3),
+                              "us_per_step": round(warm / 20 * 1e6, 2), "objective_step20": first}
+    sess.close()
     # Canonical host publication of the MLP-4096 output [4096, 4096] FLOAT32: dense and a
     # transposed view, device packing + one device-to-host copy into pageable host memory
     from synaptik_amd.backend import HipBackendIntegration, TensorDescriptor
@@ -284,31 +307,61 @@ def secondary(ctx, reps: int = 5, cpu: bool = True) -> dict:
         oracle.canonical_bytes(raw, 4, (256, WIDTH))
         dt = time.perf_counter() - t0
         out["canonical_publication"]["cpu_baseline"] = {
-            "ms_full": round(dt * BATCH / 256 * 1e3, 1), "cores": 1, "kind": "port",
+            "ms_full": round(dt * BATCH / 256 * 1e3, 1), **host_cores(), "kind": "port",
+            "extrapolated": True,
             "sample": f"oracle per-element packing of 256 of 4096 rows ({dt:.3f} s), scaled x16"}
     return out
 
 
+def host_cores() -> dict:
+    """The host's core count (nproc: the CPUs this process may run on) beside the threads used."""
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nproc = os.cpu_count() or 1
+    return {"cores": 1, "nproc": nproc}
+
+
 def add_cpu_baselines(out: dict) -> None:
-    """The oracle (1 thread) on bounded samples of the secondary configs, scaled to their units."""
+    """The oracle (1 thread) on the secondary configs: C1, C2 and C5 in full, C3 as one complete
+    1024-row Adam step (each of its 50 steps is the same work)."""
     from oracle import oracle
     from synaptik_amd.training import MlpSpec, init_parameters
     rng = np.random.default_rng(8)
-    # C5: 256 of the 65536 rows, forward (softmax, LSE) and backward
-    rows, C = 256, 4096
-    x = rng.standard_normal((rows, C), dtype=np.float32) * 2
-    g = rng.standard_normal((rows, C), dtype=np.float32)
+    # C1: the full 20-step run of 16 -> 64 -> 1 tanh, MSE, SGD 0.01, batch 256
+    spec = MlpSpec.chain([16, 64, 1], hidden="tanh", loss="mse")
+    Ws, bs = init_parameters(spec, 0, "builder")
+    model = oracle.OracleMLP(Ws, bs, ["tanh", None], "mse", dict(kind="sgd", lr=0.01))
+    x1 = rng.standard_normal((256, 16)).astype(np.float32)
+    y1 = rng.standard_normal((256, 1)).astype(np.float32)
     t0 = time.perf_counter()
-    p = oracle.softmax_rows(x)
-    oracle.logsumexp_rows(x)
-    oracle.softmax_grad_rows(p, g)
+    for _ in range(20):
+        model.step(x1, y1)
     dt = time.perf_counter() - t0
+    if "c1_plumbing_mlp" in out:
+        out["c1_plumbing_mlp"]["cpu_baseline"] = {
+            "ms_20_steps": round(dt * 1e3, 3), **host_cores(), "kind": "port",
+            "extrapolated": False, "sample": "the full 20-step run"}
+    # C5: the full [65536, 4096] forward (softmax, LSE) and backward, in 8192-row chunks (the
+    # oracle is row-wise, so the chunks do the same work as one call with a bounded footprint)
+    rows, C, chunk = 65536, 4096, 8192
+    dt = 0.0
+    for r0 in range(0, rows, chunk):
+        x = rng.standard_normal((chunk, C), dtype=np.float32) * 2
+        g = rng.standard_normal((chunk, C), dtype=np.float32)
+        t0 = time.perf_counter()
+        p = oracle.softmax_rows(x)
+        oracle.logsumexp_rows(x)
+        oracle.softmax_grad_rows(p, g)
+        dt += time.perf_counter() - t0
+    del x, g, p
     gpu_ms = out["c5_softmax_stress"]["fwd_ms"] + out["c5_softmax_stress"]["bwd_ms"]
     out["c5_softmax_stress"]["cpu_baseline"] = {
         "rows_per_s": round(rows / dt, 1), "gpu_rows_per_s": round(65536 / (gpu_ms * 1e-3), 1),
-        "cores": 1, "kind": "port", "sample": f"{rows} rows of [65536,4096], fwd+bwd, {dt:.2f} s"}
-    # C2: 256 of the 8192 rows of the fused layer, forward + both backward GEMMs + db
-    B, I, O = 256, 1024, 1024
+        "ms_full": round(dt * 1e3, 1), **host_cores(), "kind": "port", "extrapolated": False,
+        "sample": f"all 65536 rows of [65536,4096], fwd+bwd, in 8192-row chunks ({dt:.2f} s)"}
+    # C2: the full layer, 8192 rows: forward + both backward GEMMs + db
+    B, I, O = 8192, 1024, 1024
     X = rng.standard_normal((B, I), dtype=np.float32)
     W = rng.standard_normal((I, O), dtype=np.float32) * 0.05
     dY = rng.standard_normal((B, O), dtype=np.float32)
@@ -320,25 +373,22 @@ def add_cpu_baselines(out: dict) -> None:
     oracle.colsum(dZ)
     dt = time.perf_counter() - t0
     out["c2_fused_layer"]["cpu_baseline"] = {
-        "ms_full_layer": round(dt * 8192 / B * 1e3, 1), "cores": 1, "kind": "port",
-        "sample": f"{B} of 8192 rows ({dt:.2f} s), scaled x{8192 // B}"}
-    # C3: one Adam step of the classifier on 64 of the 1024 rows (+ the full update)
+        "ms_full_layer": round(dt * 1e3, 1), **host_cores(), "kind": "port",
+        "extrapolated": False, "sample": f"the full layer, {B} rows ({dt:.2f} s)"}
+    # C3: one complete Adam step of the classifier on all 1024 rows
     spec = MlpSpec.chain([784, 1024, 1024, 10], hidden="relu", loss="ce")
     Ws, bs = init_parameters(spec, 0, "he_normal")
     model = oracle.OracleMLP(Ws, bs, ["relu", "relu", None], "ce",
                              dict(kind="adam", lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8))
-    xb = rng.uniform(0, 1, (64, 784)).astype(np.float32)
-    yb = rng.integers(0, 10, 64)
+    xb = rng.uniform(0, 1, (1024, 784)).astype(np.float32)
+    yb = rng.integers(0, 10, 1024)
     t0 = time.perf_counter()
-    model.gradients(xb, yb)
-    t_fb = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    model.step(xb[:1], yb[:1])
-    t_one = time.perf_counter() - t0  # dominated by the full-parameter Adam stage
-    step_s = t_fb * 1024 / 64 + t_one
+    model.step(xb, yb)
+    step_s = time.perf_counter() - t0
     out["c3_classifier_adam"]["cpu_baseline"] = {
-        "samples_per_s": round(1024 / step_s, 1), "cores": 1, "kind": "port",
-        "sample": f"fwd+bwd on 64 of 1024 rows scaled x16 ({t_fb:.2f} s) + one full Adam step ({t_one:.2f} s)"}
+        "samples_per_s": round(1024 / step_s, 1), "ms_per_step": round(step_s * 1e3, 1),
+        **host_cores(), "kind": "port", "extrapolated": False,
+        "sample": f"one complete step (1024 rows, fwd+bwd+Adam, {step_s:.2f} s) of the 50"}
 
 
 def main() -> int:

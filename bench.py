@@ -178,6 +178,28 @@ def secondary(ctx, reps: int = 5, cpu: bool = True) -> dict:
                                        lower_dense_layer)
     out = {}
     rng = np.random.default_rng(7)
+    # The box's attainable HBM rate for one read and one write per element: the library's copy
+    # (one float4 per thread, streamed) over 1 GiB. Softmax forward moves the same bytes per
+    # element; it is reported against this figure and against the nominal 8 TB/s.
+    n = 1 << 28
+    pb = ProgramBuilder()
+    ca, cb = pb.input(n), pb.output(n)
+    pb.copy(ca, cb, n)
+    prog = HipProgram(ctx, pb.image())
+    ba, bb = ctx.buffer(n * 4), ctx.buffer(n * 4)
+    prog.run([ba], [bb])
+    prog.set_profiling(True)
+    for _ in range(reps * 4):
+        prog.run([ba], [bb])
+    t, runs = prog.step_times()
+    copy_ms = t[0] / runs
+    copy_gbs = 2 * n * 4 / copy_ms / 1e6
+    out["hbm_copy_ceiling"] = {"bytes": 2 * n * 4, "ms": round(copy_ms, 4),
+                               "GBps": round(copy_gbs, 1),
+                               "frac_hbm": round(copy_gbs / HBM_PEAK_GBS, 4)}
+    prog.close()
+    ba.close()
+    bb.close()
     # C5: softmax + LSE + mean forward, softmax-with-LSE-cotangent backward over [65536, 4096]
     R, C = 65536, 4096
     pb = ProgramBuilder()
@@ -205,7 +227,9 @@ def secondary(ctx, reps: int = 5, cpu: bool = True) -> dict:
         "shape": [R, C], "fwd_ms": round(fwd_ms, 4), "mean_ms": round(mean_ms, 4), "bwd_ms": round(bwd_ms, 4),
         "fwd_GBps": round(fwd_bytes / fwd_ms / 1e6, 1), "bwd_GBps": round(bwd_bytes / bwd_ms / 1e6, 1),
         "fwd_frac_hbm": round(fwd_bytes / fwd_ms / 1e6 / HBM_PEAK_GBS, 4),
-        "bwd_frac_hbm": round(bwd_bytes / bwd_ms / 1e6 / HBM_PEAK_GBS, 4)}
+        "bwd_frac_hbm": round(bwd_bytes / bwd_ms / 1e6 / HBM_PEAK_GBS, 4),
+        "fwd_frac_copy": round(fwd_bytes / fwd_ms / 1e6 / copy_gbs, 4),
+        "bwd_frac_copy": round(bwd_bytes / bwd_ms / 1e6 / copy_gbs, 4)}
     prog.close()
     for b in (bx, bdp, bp, bdx):
         b.close()

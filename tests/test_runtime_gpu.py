@@ -110,3 +110,24 @@ def test_program_is_reusable_and_arena_persists_between_runs(ctx):
     times, runs = prog.step_times()
     assert runs == 1 and len(times) == 2 and all(t > 0 for t in times)
     prog.close()
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 1023, 1_000_003, 1 << 24])
+def test_copy_is_bit_exact_for_ragged_lengths(ctx, n):
+    # the vector body copies whole float4s, the scalar tail the last n % 4 elements; NaN
+    # payloads and signed zeros must come through unchanged (the copy moves bits, not values)
+    rng = np.random.default_rng(n)
+    bits = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+    bits[: min(n, 4)] = [0x7FC00001, 0x80000000, 0xFF800000, 0x00000001][: min(n, 4)]
+    src = bits.view(np.float32)
+    pb = ProgramBuilder()
+    x, y = pb.input(n), pb.output(n + 4)
+    pb.fill(y, n + 4, 7.0)
+    pb.copy(x, y, n)
+    prog = HipProgram(ctx, pb.image())
+    bx, by = ctx.upload(src), ctx.buffer((n + 4) * 4)
+    prog.run([bx], [by])
+    got = by.download().view(np.uint32)
+    assert np.array_equal(got[:n], bits)
+    assert np.all(by.download()[n:] == 7.0)  # nothing written past the copied range
+    prog.close()

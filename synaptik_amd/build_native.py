@@ -21,7 +21,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # the per-layout GEMM units are the slowest to compile and go first
 SOURCES = ["gemm_nn.hip", "gemm_nt.hip", "gemm_tn.hip", "gemm_tt.hip", "gemm.hip", "gemm_skinny.hip",
-           "elementwise.hip", "softmax_loss.hip", "optim.hip", "publish.hip", "runtime.cpp", "lxm.cpp"]
+           "elementwise.hip", "softmax_loss.hip", "ce_head.hip", "optim.hip", "publish.hip", "runtime.cpp", "lxm.cpp"]
 
 COMMON_FLAGS = [
     "--offload-arch=gfx950",

@@ -115,6 +115,28 @@ hipError_t launch_index_ce(const float* logits, const void* target, int target_i
                            hipStream_t s);
 int64_t index_ce_partial_doubles(int64_t R);
 
+// Fused classifier head (J <= 16 classes, MEAN index cross-entropy without an ignore index):
+// logits = H . W^T + b, row_loss[r], dz = (softmax - onehot) * (g / R) and, when dx is set,
+// dx = act_grad(act, dz . W, H), each bit-identical to the unfused row-dot GEMM, CE and small-K
+// GEMM sequence. H [R, K], W [J, K], bias [J] (optional), logits [R, J] (optional), dz [R, J].
+struct CeHeadParams {
+  const float* H;
+  const float* W;
+  const float* bias;
+  const void* target;
+  float* logits;
+  float* dz;
+  float* dx;
+  float* row_loss;
+  uint32_t* status;
+  int64_t R, K;
+  int J, act, target_is_64, vec;
+  float g;
+};
+hipError_t launch_ce_head(const CeHeadParams& p, hipStream_t s);
+// loss[0] = MEAN of row_loss[0 .. R) (binary64 sum, one rounding, divided by R).
+hipError_t launch_ce_head_finish(const float* row_loss, int64_t R, float* loss, hipStream_t s);
+
 // Interpreted fused elementwise chain (see pointwise.hip for the instruction set).
 struct PwInstr {
   uint8_t op, dst, a, b;

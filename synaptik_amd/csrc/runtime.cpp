@@ -179,6 +179,7 @@ enum Opcode : uint32_t {
   OP_FILL = 13,
   OP_COPY = 14,
   OP_TRANSPOSE = 15,
+  OP_CE_HEAD = 16,
 };
 
 #pragma pack(push, 1)
@@ -567,6 +568,45 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
       need((uint64_t)shk::index_ce_partial_doubles(R));
       return SHK_HIP_STATUS_OK;
     }
+    case OP_CE_HEAD: {
+      const int64_t R = a[0], K = a[1], J = a[2], act = a[3], phase = a[4], is64 = a[5];
+      if (phase == 1) {
+        if (R < 0) return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid head loss", idx);
+        if (!v.slot_ok(s[0], false, "row losses") || !v.slot_ok(s[1], false, "loss") ||
+            !v.holds(s[0], R, DT_F32, "row losses") || !v.holds(s[1], 1, DT_F32, "loss") ||
+            !v.writable(s[1], "loss"))
+          return v.err;
+        if (s[0] == s[1])
+          return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: head loss aliases its input", idx);
+        return SHK_HIP_STATUS_OK;
+      }
+      if (phase != 0 || R < 0 || K <= 0 || J < 1 || J > 16 || act < 0 || act > 3 ||
+          (is64 != 0 && is64 != 1))
+        return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid classifier head", idx);
+      if (!v.slot_ok(s[0], false, "head input") || !v.slot_ok(s[1], false, "head weight") ||
+          !v.slot_ok(s[2], true, "head bias") || !v.slot_ok(s[3], false, "target") ||
+          !v.slot_ok(s[4], true, "logits") || !v.slot_ok(s[5], false, "logit cotangent") ||
+          !v.slot_ok(s[6], true, "input cotangent") || !v.slot_ok(s[7], false, "row losses") ||
+          !v.holds(s[0], prod(R, K), DT_F32, "head input") ||
+          !v.holds(s[1], prod(J, K), DT_F32, "head weight") || !v.holds(s[2], J, DT_F32, "head bias") ||
+          !v.holds(s[3], R, is64 ? DT_I64 : DT_I32, "target") ||
+          !v.holds(s[4], prod(R, J), DT_F32, "logits") ||
+          !v.holds(s[5], prod(R, J), DT_F32, "logit cotangent") ||
+          !v.holds(s[6], prod(R, K), DT_F32, "input cotangent") ||
+          !v.holds(s[7], R, DT_F32, "row losses") || !v.writable(s[4], "logits") ||
+          !v.writable(s[5], "logit cotangent") || !v.writable(s[6], "input cotangent") ||
+          !v.writable(s[7], "row losses"))
+        return v.err;
+      // the written slots are distinct from each other and from every slot the head reads
+      for (int i = 4; i < 8; ++i) {
+        if (s[i] < 0) continue;
+        for (int k = 0; k < 8; ++k)
+          if (k != i && s[k] == s[i])
+            return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED,
+                        "step %zu: classifier head slot %d is used twice", idx, s[i]);
+      }
+      return SHK_HIP_STATUS_OK;
+    }
     case OP_OPTIMIZER: {
       const int64_t kind = a[0], phase = a[1];
       if (kind < 0 || kind > 5 || phase < 0 || phase > 2 || (phase == 2 && kind > 2))
@@ -715,6 +755,22 @@ hipError_t enqueue_step(const Step& st, const Bound& b, hipStream_t stream, doub
       return shk::launch_index_ce(b.get<const float>(s[0]), b.get<const void>(s[1]), (int)a[2],
                                   b.get<float>(s[2]), b.get<float>(s[3]), a[0], a[1], (int)a[3], a[4],
                                   r.farg[0], scratch, status, stream);
+    case OP_CE_HEAD: {
+      if (a[4] == 1) return shk::launch_ce_head_finish(b.get<const float>(s[0]), a[0], b.get<float>(s[1]), stream);
+      shk::CeHeadParams p{};
+      p.H = b.get<const float>(s[0]);
+      p.W = b.get<const float>(s[1]);
+      p.bias = b.get<const float>(s[2]);
+      p.target = b.get<const void>(s[3]);
+      p.logits = b.get<float>(s[4]);
+      p.dz = b.get<float>(s[5]);
+      p.dx = b.get<float>(s[6]);
+      p.row_loss = b.get<float>(s[7]);
+      p.status = status;
+      p.R = a[0]; p.K = a[1]; p.J = (int)a[2]; p.act = (int)a[3]; p.target_is_64 = (int)a[5];
+      p.g = r.farg[0];
+      return shk::launch_ce_head(p, stream);
+    }
     case OP_OPTIMIZER: {
       shk::OptParams p{};
       const OptEntry* e = reinterpret_cast<const OptEntry*>(st.payload.data());
@@ -784,6 +840,11 @@ Access step_access(const Step& st) {
     case OP_LSE_BWD: R(sl[0]); R(sl[1]); R(sl[2]); W(sl[3]); break;
     case OP_MSE: R(sl[0]); R(sl[1]); W(sl[2]); W(sl[3]); break;
     case OP_CE_INDEX: R(sl[0]); R(sl[1]); W(sl[2]); W(sl[3]); x.status_or = true; break;
+    case OP_CE_HEAD:
+      if (a[4] == 1) { R(sl[0]); W(sl[1]); break; }
+      R(sl[0]); R(sl[1]); R(sl[2]); R(sl[3]); W(sl[4]); W(sl[5]); W(sl[6]); W(sl[7]);
+      x.status_or = true;
+      break;
     case OP_OPTIMIZER: {
       const OptEntry* e = reinterpret_cast<const OptEntry*>(st.payload.data());
       const size_t n = st.payload.size() / sizeof(OptEntry);

@@ -42,6 +42,7 @@ OP_STEP_COMMIT = 12
 OP_FILL = 13
 OP_COPY = 14
 OP_TRANSPOSE = 15
+OP_CE_HEAD = 16
 
 ACT = {None: 0, "none": 0, "relu": 1, "tanh": 2, "sigmoid": 3}
 REDUCE_KIND = {"sum": 0, "mean": 1, "max": 2, "lse": 3}
@@ -200,6 +201,20 @@ class ProgramBuilder:
         return self._add(OP_CE_INDEX, [logits, target, loss, grad],
                          [R, C, is64, 0 if ignore_index is None else 1,
                           0 if ignore_index is None else ignore_index], [g])
+
+    def ce_head(self, H, W, target, dz, row_loss, R, K, J, *, bias=None, logits=None, dx=None,
+                act=None, g=1.0) -> Step:
+        """Classifier head of a training step: logits = H . W^T + bias ([R, J], stored when
+        `logits` is given), per-row index cross-entropy into `row_loss`, the logit cotangent
+        dz = (softmax - onehot) * (g / R) and, when `dx` is given, the input cotangent
+        act_grad(act, dz . W, H). J <= 16; MEAN without an ignore index."""
+        is64 = 1 if (isinstance(target, Slot) and target.dtype == "i64") else 0
+        return self._add(OP_CE_HEAD, [H, W, bias, target, logits, dz, dx, row_loss],
+                         [R, K, J, ACT[act], 0, is64], [g])
+
+    def ce_head_loss(self, row_loss, loss, R) -> Step:
+        """MEAN of the head's per-row losses into loss[0]."""
+        return self._add(OP_CE_HEAD, [row_loss, loss], [R, 0, 0, 0, 1])
 
     def optimizer(self, counter, tensors, *, kind: str, phase: int, lr: float, momentum=0.0,
                   dampening=0.0, weight_decay=0.0, nesterov=False, has_momentum_slot=False,

@@ -34,6 +34,9 @@ FUSE_BIAS_GRADIENT = True
 # In RESET_AND_STEP runs, stage each weight's optimizer update in the epilogue of the GEMM that
 # computes its gradient (the gradient is never stored and the weights skip the streaming pass).
 FUSE_OPTIMIZER = True
+# Lower a cross-entropy head of at most 16 classes to one fused step (logits, per-row loss, the
+# logit cotangent and the cotangent of the head's input; bit-identical to the unfused steps).
+FUSE_CE_HEAD = True
 
 
 class GradientMode:
@@ -253,26 +256,40 @@ def lower_training_step(spec: MlpSpec, batch: int, optimizer, *, label_dtype: st
 
     # activations Y_l (internal); Y_0 is the input x
     acts = [lay.x] + [pb.internal(batch * l.fan_out) for l in spec.layers]
-    widest = max(l.fan_out for l in spec.layers)
-    dz = [pb.internal(batch * widest), pb.internal(batch * widest)]
+    # one cotangent buffer per layer: reusing a buffer two layers apart would make the input
+    # gradient of a layer wait (write after read) for the weight gradient of the layer above it,
+    # serializing the two streams' work
+    dz = [pb.internal(batch * l.fan_out) for l in spec.layers]
     gW = [pb.internal(l.fan_in * l.fan_out) for l in spec.layers]
     gb = [pb.internal(l.fan_out) if l.bias else None for l in spec.layers]
     lay.grads = gW + [g for g in gb if g is not None]
 
+    # A cross-entropy head of at most 16 classes is one fused step (logits, loss, both
+    # cotangents); its forward GEMM is not emitted separately.
+    head = FUSE_CE_HEAD and spec.loss == "ce" and out_w <= 16
     # forward
-    for i, l in enumerate(spec.layers):
+    for i, l in enumerate(spec.layers[: L - 1] if head else spec.layers):
         pb.gemm(acts[i], lay.weights[i], acts[i + 1], batch, l.fan_out, l.fan_in, trans_b=True,
                 bias=lay.biases[i], act=l.activation)
     # objective and its cotangent (g = 1)
-    cur = dz[0]
+    if spec.layers[-1].activation is not None:
+        raise ValueError("the loss heads are lowered for an identity output layer "
+                         "(cross-entropy consumes raw logits)")
+    dx_done = False  # the head also produced the cotangent of the last layer's input
+    head_loss = None
     if spec.loss == "mse":
-        if spec.layers[-1].activation is not None:
-            raise ValueError("the MSE head is lowered for an identity output layer")
-        pb.mse(acts[L], lay.y, lay.loss, batch * out_w, grad=cur, reduction=spec.reduction)
+        pb.mse(acts[L], lay.y, lay.loss, batch * out_w, grad=dz[L - 1], reduction=spec.reduction)
+    elif head:
+        row_loss = pb.internal(batch)
+        last = spec.layers[-1]
+        pb.ce_head(acts[L - 1], lay.weights[L - 1], lay.y, dz[L - 1], row_loss, batch,
+                   last.fan_in, out_w, bias=lay.biases[L - 1],
+                   dx=dz[L - 2] if L > 1 else None,
+                   act=spec.layers[L - 2].activation if L > 1 else None)
+        head_loss = (row_loss, lay.loss, batch)
+        dx_done = L > 1
     else:
-        if spec.layers[-1].activation is not None:
-            raise ValueError("cross-entropy consumes raw logits")
-        pb.index_ce(acts[L], lay.y, lay.loss, batch, out_w, grad=cur)
+        pb.index_ce(acts[L], lay.y, lay.loss, batch, out_w, grad=dz[L - 1])
     common = {}
     if kind == "sgd":
         common = dict(lr=optimizer.learning_rate, momentum=optimizer.momentum,
@@ -282,33 +299,37 @@ def lower_training_step(spec: MlpSpec, batch: int, optimizer, *, label_dtype: st
         common = dict(lr=optimizer.learning_rate, beta1=optimizer.beta1, beta2=optimizer.beta2,
                       eps=optimizer.epsilon, weight_decay=optimizer.weight_decay)
     fuse_update = FUSE_OPTIMIZER and mode == GradientMode.RESET_AND_STEP
-    # backward
-    db_done = False  # the bias gradient of the current dZ was fused into the GEMM producing it
+    # backward. The two-stream plan keeps a step on the main stream when it depends on the main
+    # stream's latest step, so the emission order shapes the schedule: first the chain of input
+    # cotangents (each layer's waits on the one above), then every layer's weight and bias
+    # gradients, which start as soon as their own cotangent exists and run beside the chain.
+    db_fused = [False] * L  # db_i was summed in the epilogue of the GEMM producing dZ_i
+    for i in reversed(range(1, L)):
+        if dx_done and i == L - 1:
+            continue
+        l, prev = spec.layers[i], spec.layers[i - 1]
+        # dZ_{i-1} = act_grad(dZ_i . W_i, Y_{i-1}), with db_{i-1} = SUM_TO_SHAPE(dZ_{i-1}) summed
+        # in the same epilogue
+        fuse = FUSE_BIAS_GRADIENT and gb[i - 1] is not None
+        pb.gemm(dz[i], lay.weights[i], dz[i - 1], batch, l.fan_in, l.fan_out, aux=acts[i],
+                act=prev.activation or "none", act_grad=True, colsum=gb[i - 1] if fuse else None)
+        db_fused[i - 1] = fuse
     for i in reversed(range(L)):
         l = spec.layers[i]
         # dW[out,in] = dZ^T . X   (PERMUTE of X^T.dZ absorbed)
         if fuse_update:
-            pb.gemm_update(cur, acts[i], l.fan_out, l.fan_in, batch, lay.counter,
+            pb.gemm_update(dz[i], acts[i], l.fan_out, l.fan_in, batch, lay.counter,
                            (lay.weights[i], lay.first[i] if has_first else None,
                             lay.second[i] if lay.second else None, lay.weights_next[i],
                             lay.first_next[i] if has_first else None,
                             lay.second_next[i] if lay.second else None),
                            kind=kind, trans_a=True, **common)
         else:
-            pb.gemm(cur, acts[i], gW[i], l.fan_out, l.fan_in, batch, trans_a=True)
-        if gb[i] is not None and not db_done:
-            pb.colsum(cur, gb[i], batch, l.fan_out)
-        db_done = False
-        if i > 0:
-            nxt = dz[1] if cur is dz[0] else dz[0]
-            prev = spec.layers[i - 1]
-            # dZ_{i-1} = act_grad(dZ_i . W_i, Y_{i-1}), with db_{i-1} = SUM_TO_SHAPE(dZ_{i-1})
-            # summed in the same epilogue
-            fuse = FUSE_BIAS_GRADIENT and gb[i - 1] is not None
-            pb.gemm(cur, lay.weights[i], nxt, batch, l.fan_in, l.fan_out, aux=acts[i],
-                    act=prev.activation or "none", act_grad=True, colsum=gb[i - 1] if fuse else None)
-            db_done = fuse
-            cur = nxt
+            pb.gemm(dz[i], acts[i], gW[i], l.fan_out, l.fan_in, batch, trans_a=True)
+        if gb[i] is not None and not db_fused[i]:
+            pb.colsum(dz[i], gb[i], batch, l.fan_out)
+    if head_loss is not None:
+        pb.ce_head_loss(*head_loss)  # nothing waits on the objective but the commit
     if mode != GradientMode.RESET_AND_STEP:
         # G = accumulator + G for every tensor, each candidate checked finite
         acc_entries = [(g, g, a, None, g.count) for g, a in zip(lay.grads, lay.accum)]

@@ -154,3 +154,35 @@ def test_image_validation_without_a_device():
     pb.row_reduce(x, y, 2**31 - 1, 2**40, "sum")
     with pytest.raises(HipInvalidArgument):
         validate_program_image(pb.image())
+
+
+def test_classifier_head_step_validation_without_a_device():
+    """The fused classifier head step: a well-formed head validates; more than 16 classes, an
+    unknown activation or phase, a written slot used twice, a read-only output and short slots
+    are refused at decode time."""
+    from synaptik_amd.native import HipBackendError, validate_program_image
+
+    def head(R=8, K=12, J=4, act="relu", reuse=False, short=False, phase=None, ro=False):
+        pb = ProgramBuilder()
+        H, W, b = pb.input(R * K), pb.input(J * K - (1 if short else 0)), pb.input(J)
+        t = pb.input(R, "i64")
+        dz = pb.input(R * J) if ro else pb.internal(R * J)
+        dx = dz if reuse else pb.internal(R * K)
+        rl, loss = pb.internal(R), pb.output(1)
+        st = pb.ce_head(H, W, t, dz, rl, R, K, J, bias=b, dx=dx, act=act)
+        if phase is not None:
+            st.iargs[4] = phase
+        pb.ce_head_loss(rl, loss, R)
+        return pb.image()
+
+    assert validate_program_image(head()) > 0
+    assert validate_program_image(head(J=16, K=9)) > 0
+    for bad in (dict(J=17), dict(J=0), dict(reuse=True), dict(short=True), dict(phase=2),
+                dict(ro=True)):
+        with pytest.raises(HipBackendError):
+            validate_program_image(head(**bad))
+    pb = ProgramBuilder()
+    rl = pb.internal(8)
+    pb.ce_head_loss(rl, rl, 8)  # the loss may not alias its input
+    with pytest.raises(HipBackendError):
+        validate_program_image(pb.image())

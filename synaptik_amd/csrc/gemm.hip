@@ -69,6 +69,20 @@ __global__ void __launch_bounds__(256) gemm_k1_outer(GemmParams p) {
   if (upd) update_flag(p.upd, uc, ok);
 }
 
+// dz = act_grad(act, dy, y) over an [M, N] view (dy and dz with leading dimension ld, y with ldy):
+// the second output of a forward GEMM with its cotangent (mode 2) on routes whose epilogue does
+// not form it.
+__global__ void __launch_bounds__(256) gemm_cotangent_pass(const float* __restrict__ y, int64_t ldy,
+                                                           const float* __restrict__ dy,
+                                                           float* __restrict__ dz, int64_t ld,
+                                                           int64_t M, int64_t N, int act) {
+  const int64_t total = M * N;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int64_t row = e / N, col = e - row * N;
+    dz[row * ld + col] = act_grad(act, dy[row * ld + col], y[row * ldy + col]);
+  }
+}
+
 // Split-K reduction: sums the slices of each output in slice order (a fixed binary32 order, so
 // results are deterministic) and applies the GEMM epilogue.
 __global__ void __launch_bounds__(256) gemm_splitk_reduce(GemmParams p, int splits) {
@@ -255,6 +269,24 @@ hipError_t launch_gemm_core(const GemmParams& in, float* workspace, hipStream_t 
 hipError_t launch_gemm(const GemmParams& in, float* workspace, hipStream_t s) {
   GemmParams p = in;
   p.colsum_partial = nullptr;
+  if (p.mode == 2 && p.M > 0 && p.N > 0 &&
+      (p.K <= 1 || use_split(p, workspace != nullptr) || skinny_route(p) != SKINNY_NONE)) {
+    // Mode 2 on a route without the tile kernels' epilogue: the plain forward GEMM, then the
+    // cotangent pass and (optionally) its column sum.
+    GemmParams f = p;
+    f.mode = 0;
+    f.aux = nullptr;
+    f.dz = nullptr;
+    f.colsum = nullptr;
+    hipError_t e = launch_gemm_core(f, workspace, s);
+    if (e != hipSuccess) return e;
+    const unsigned blocks = (unsigned)std::min<int64_t>(65536, (p.M * p.N + 255) / 256);
+    hipLaunchKernelGGL(gemm_cotangent_pass, dim3(blocks), dim3(256), 0, s, p.C, p.ldc, p.aux,
+                       p.dz, p.ldaux, p.M, p.N, p.act);
+    if ((e = hipGetLastError()) != hipSuccess || p.colsum == nullptr) return e;
+    return launch_colsum(p.dz, p.colsum, p.M, p.N, p.ldaux, 1.0, 0,
+                         reinterpret_cast<double*>(workspace), s);
+  }
   if (p.colsum == nullptr || p.M <= 0 || p.N <= 0) return launch_gemm_core(p, workspace, s);
   const bool split = use_split(p, workspace != nullptr);
   const SkinnyRoute route = skinny_route(p);

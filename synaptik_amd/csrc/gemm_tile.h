@@ -340,13 +340,13 @@ gemm_f32_mfma(GemmParams p) {
     static_for<MI>([&](auto i) {
       const int64_t row0 = m0 + wm * (MI * 32) + i * 32 + half * 4;
       float* cptr = p.C + row0 * p.ldc + col;
-      const float* aptr = p.mode == 1 ? p.aux + row0 * p.ldaux + col : nullptr;
+      const float* aptr = p.mode != 0 ? p.aux + row0 * p.ldaux + col : nullptr;
       static_for<16>([&](auto r) {
         constexpr int R = decltype(r)::value;
         constexpr int off = (R >> 2) * 8 + (R & 3);
         if (col_ok && row0 + off < p.M) {
           float v = acc[i][j][R];
-          if (p.mode == 0) {
+          if (p.mode != 1) {
             if (p.bias != nullptr) v = v + bias;
             v = apply_act(p.act, v);
           } else {
@@ -355,6 +355,10 @@ gemm_f32_mfma(GemmParams p) {
           float* dst = cptr + off * p.ldc;
           if (p.accumulate) v = *dst + v;
           *dst = v;
+          if (p.mode == 2) {  // the activation input's cotangent from dY (aux) and the output
+            v = act_grad(p.act, aptr[off * p.ldaux], v);
+            p.dz[(row0 + off) * p.ldaux + col] = v;
+          }
           csum += (double)v;
         }
       });

@@ -27,6 +27,7 @@
 // reassociate anyway (the reference contract allows it, foundational-modules.md:423-425).
 #pragma once
 #include <cstdlib>
+#include <type_traits>
 
 #include "gemm_tile.h"
 #include "gemm_v2_layout.h"
@@ -464,60 +465,96 @@ gemm_f32_v2(GemmParams p) {
   };
   const int64_t row_e = m0 + wm * WT + rg, col_e = n0 + wn * WT + 4 * q;
   const bool col_ok = !TAIL || col_e < p.N;  // N is a multiple of 4: whole segments
+  // The loops below are compiled once per optimizer kind / (mode, activation, accumulate): a
+  // runtime switch inside them would make every LDS read and store wait for the one before.
   if (p.upd.pn != nullptr) {
     const GemmUpdate& u = p.upd;
     const UpdateCtx uc = update_ctx(u);
     bool ok = uc.k.ok;
-    for (int t = 0; t < WT / RSTEP; ++t) {
-      const int64_t row = row_e + RSTEP * t;
-      if (TAIL && (!col_ok || row >= p.M)) continue;
-      const int64_t e = row * p.N + col_e;
-      const floatx4 gv = tile_row(t);
-      const floatx4 pv = *reinterpret_cast<const floatx4*>(u.p + e);
-      const floatx4 mv = u.m != nullptr ? *reinterpret_cast<const floatx4*>(u.m + e) : floatx4{0.f, 0.f, 0.f, 0.f};
-      const floatx4 vv = u.kind != 0 ? *reinterpret_cast<const floatx4*>(u.v + e) : floatx4{0.f, 0.f, 0.f, 0.f};
-      floatx4 pc, mc, vc = floatx4{0.f, 0.f, 0.f, 0.f};
-      static_for<4>([&](auto c) {
-        constexpr int C = decltype(c)::value;
-        float pe, me, ve = 0.0f;
-        if (u.kind == 0) ok &= sgd_element(u, uc.first, pv[C], gv[C], mv[C], pe, me);
-        else ok &= adam_element(u, uc.k, pv[C], gv[C], mv[C], vv[C], pe, me, ve);
-        pc[C] = pe;
-        mc[C] = me;
-        vc[C] = ve;
-      });
-      *reinterpret_cast<floatx4*>(u.pn + e) = pc;
-      if (u.mn != nullptr) *reinterpret_cast<floatx4*>(u.mn + e) = mc;
-      if (u.kind != 0) *reinterpret_cast<floatx4*>(u.vn + e) = vc;
-    }
+    auto update_rows = [&](auto kindc) {
+      constexpr bool SGD = decltype(kindc)::value == 0;
+      for (int t = 0; t < WT / RSTEP; ++t) {
+        const int64_t row = row_e + RSTEP * t;
+        if (TAIL && (!col_ok || row >= p.M)) continue;
+        const int64_t e = row * p.N + col_e;
+        const floatx4 gv = tile_row(t);
+        const floatx4 pv = *reinterpret_cast<const floatx4*>(u.p + e);
+        const floatx4 mv = u.m != nullptr ? *reinterpret_cast<const floatx4*>(u.m + e) : floatx4{0.f, 0.f, 0.f, 0.f};
+        const floatx4 vv = SGD ? floatx4{0.f, 0.f, 0.f, 0.f} : *reinterpret_cast<const floatx4*>(u.v + e);
+        floatx4 pc, mc, vc = floatx4{0.f, 0.f, 0.f, 0.f};
+        static_for<4>([&](auto c) {
+          constexpr int C = decltype(c)::value;
+          float pe, me, ve = 0.0f;
+          if constexpr (SGD) ok &= sgd_element(u, uc.first, pv[C], gv[C], mv[C], pe, me);
+          else ok &= adam_element(u, uc.k, pv[C], gv[C], mv[C], vv[C], pe, me, ve);
+          pc[C] = pe;
+          mc[C] = me;
+          vc[C] = ve;
+        });
+        *reinterpret_cast<floatx4*>(u.pn + e) = pc;
+        if (u.mn != nullptr) *reinterpret_cast<floatx4*>(u.mn + e) = mc;
+        if constexpr (!SGD) *reinterpret_cast<floatx4*>(u.vn + e) = vc;
+      }
+    };
+    if (u.kind == 0) update_rows(std::integral_constant<int, 0>{});
+    else update_rows(std::integral_constant<int, 1>{});
     update_flag(u, uc, ok);
     return;
   }
+  const bool has_bias = p.bias != nullptr;
   floatx4 bias = floatx4{0.f, 0.f, 0.f, 0.f};
-  if (p.bias != nullptr && col_ok) bias = *reinterpret_cast<const floatx4*>(p.bias + col_e);
+  if (has_bias && col_ok) bias = *reinterpret_cast<const floatx4*>(p.bias + col_e);
   double cs[4] = {0.0, 0.0, 0.0, 0.0};  // fused column sums of this lane's stored values
-  for (int t = 0; t < WT / RSTEP; ++t) {
-    const int64_t row = row_e + RSTEP * t;
-    if (TAIL && (!col_ok || row >= p.M)) continue;
-    floatx4 v = tile_row(t);
-    if (p.mode == 0) {
-      if (p.bias != nullptr) v = floatx4{v[0] + bias[0], v[1] + bias[1], v[2] + bias[2], v[3] + bias[3]};
-      static_for<4>([&](auto c) { v[decltype(c)::value] = apply_act(p.act, v[decltype(c)::value]); });
-    } else {
-      const floatx4 y = *reinterpret_cast<const floatx4*>(p.aux + row * p.ldaux + col_e);
-      static_for<4>([&](auto c) {
-        constexpr int C = decltype(c)::value;
-        v[C] = act_grad(p.act, v[C], y[C]);
-      });
+  auto store_rows = [&](auto modec, auto actc, auto accc) {
+    constexpr int MODE = decltype(modec)::value, ACT = decltype(actc)::value;
+    constexpr bool ACC = decltype(accc)::value;
+    for (int t = 0; t < WT / RSTEP; ++t) {
+      const int64_t row = row_e + RSTEP * t;
+      if (TAIL && (!col_ok || row >= p.M)) continue;
+      floatx4 v = tile_row(t);
+      if constexpr (MODE != 1) {
+        if (has_bias) v = floatx4{v[0] + bias[0], v[1] + bias[1], v[2] + bias[2], v[3] + bias[3]};
+        static_for<4>([&](auto c) { v[decltype(c)::value] = apply_act(ACT, v[decltype(c)::value]); });
+      } else {
+        const floatx4 y = *reinterpret_cast<const floatx4*>(p.aux + row * p.ldaux + col_e);
+        static_for<4>([&](auto c) {
+          constexpr int C = decltype(c)::value;
+          v[C] = act_grad(ACT, v[C], y[C]);
+        });
+      }
+      floatx4* dst = reinterpret_cast<floatx4*>(p.C + row * p.ldc + col_e);
+      if constexpr (ACC) {
+        const floatx4 o = *dst;
+        v = floatx4{o[0] + v[0], o[1] + v[1], o[2] + v[2], o[3] + v[3]};
+      }
+      *dst = v;
+      if constexpr (MODE == 2) {
+        // the cotangent of the activation input from the stored activation and dY
+        const floatx4 gy = *reinterpret_cast<const floatx4*>(p.aux + row * p.ldaux + col_e);
+        static_for<4>([&](auto c) {
+          constexpr int C = decltype(c)::value;
+          v[C] = act_grad(ACT, gy[C], v[C]);
+        });
+        *reinterpret_cast<floatx4*>(p.dz + row * p.ldaux + col_e) = v;
+      }
+      static_for<4>([&](auto c) { cs[decltype(c)::value] += (double)v[decltype(c)::value]; });
     }
-    floatx4* dst = reinterpret_cast<floatx4*>(p.C + row * p.ldc + col_e);
-    if (p.accumulate) {
-      const floatx4 o = *dst;
-      v = floatx4{o[0] + v[0], o[1] + v[1], o[2] + v[2], o[3] + v[3]};
+  };
+  auto by_acc = [&](auto modec, auto actc) {
+    if (p.accumulate) store_rows(modec, actc, std::true_type{});
+    else store_rows(modec, actc, std::false_type{});
+  };
+  auto by_act = [&](auto modec) {
+    switch (p.act) {
+      case ACT_RELU: by_acc(modec, std::integral_constant<int, ACT_RELU>{}); break;
+      case ACT_TANH: by_acc(modec, std::integral_constant<int, ACT_TANH>{}); break;
+      case ACT_SIGMOID: by_acc(modec, std::integral_constant<int, ACT_SIGMOID>{}); break;
+      default: by_acc(modec, std::integral_constant<int, ACT_NONE>{}); break;
     }
-    *dst = v;
-    static_for<4>([&](auto c) { cs[decltype(c)::value] += (double)v[decltype(c)::value]; });
-  }
+  };
+  if (p.mode == 0) by_act(std::integral_constant<int, 0>{});
+  else if (p.mode == 1) by_act(std::integral_constant<int, 1>{});
+  else by_act(std::integral_constant<int, 2>{});
   if (p.colsum_partial != nullptr) {
     // lanes q + ECPR rg hold the same columns: one partial row per wave
     static_for<4>([&](auto c) {
@@ -568,7 +605,8 @@ inline int v2_choose(const GemmParams& p, bool va, bool vb) {
       return 0;
   } else {
     if (!al(p.C) || p.ldc % 4 != 0 || (p.bias != nullptr && !al(p.bias))) return 0;
-    if (p.mode == 1 && (!al(p.aux) || p.ldaux % 4 != 0)) return 0;
+    if (p.mode != 0 && (!al(p.aux) || p.ldaux % 4 != 0)) return 0;
+    if (p.mode == 2 && !al(p.dz)) return 0;
   }
   const int64_t ld = std::max(p.lda, p.ldb);
   if ((p.M + 128) * ld >= (1LL << 31) || (p.N + 128) * ld >= (1LL << 31) ||

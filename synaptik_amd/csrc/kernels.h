@@ -21,6 +21,9 @@ enum DeviceStatus : uint32_t {
 //   transB = 0: B is row-major [K,N] (N contiguous), transB = 1: B is stored [N,K].
 //   mode 0 (forward):  C = act(acc + bias)             (bias optional, act in Act)
 //   mode 1 (backward): C = act_grad(act, acc, aux)       (aux = activation output y)
+//   mode 2 (forward with its cotangent): C = act(acc + bias) as mode 0, and with aux = dY (the
+//          upstream cotangent of C, leading dimension ldaux) also dz = act_grad(act, dY, C)
+//          (same leading dimension); the optional column sum then sums dz, not C.
 //   accumulate != 0:   the epilogue value is added to the existing C (gradient accumulation).
 // Optimizer update fused into a GEMM epilogue that produces a weight gradient: the epilogue
 // stages the candidate parameter and slots exactly as the streaming optimizer's phase 2 (same
@@ -60,6 +63,8 @@ struct GemmParams {
   // receives the sum over all M rows; colsum_partial is launch_gemm's workspace.
   float* colsum;
   double* colsum_partial;
+  // mode 2: the cotangent of the activation input, [M, N] with leading dimension ldaux
+  float* dz;
   // Optional fused optimizer update (C is then not written and may be null; requires ldc == N,
   // mode 0, no bias, no activation, no accumulate, no column sum).
   GemmUpdate upd;

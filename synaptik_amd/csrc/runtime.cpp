@@ -415,17 +415,34 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
       const int64_t M = a[0], N = a[1], K = a[2], lda = a[3], ldb = a[4], ldc = a[5], ldaux = a[6];
       const int64_t tA = a[7], tB = a[8], act = a[9], mode = a[10];
       if (M < 0 || N < 0 || K < 0 || (tA != 0 && tA != 1) || (tB != 0 && tB != 1) || act < 0 ||
-          act > 3 || (mode != 0 && mode != 1))
+          act > 3 || mode < 0 || mode > 2)
         return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: invalid GEMM attributes", idx);
       if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX)
         return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: GEMM extent too large", idx);
       const bool empty = M == 0 || N == 0;  // touches no memory
       if (!empty && ((K > 0 && (tA ? lda < std::max<int64_t>(M, 1) : lda < K)) ||
           (K > 0 && (tB ? ldb < K : ldb < std::max<int64_t>(N, 1))) ||
-          ldc < std::max<int64_t>(N, 1) || (mode == 1 && ldaux < std::max<int64_t>(N, 1))))
+          ldc < std::max<int64_t>(N, 1) || (mode != 0 && ldaux < std::max<int64_t>(N, 1))))
         return fail(SHK_HIP_STATUS_UNSUPPORTED_SHAPE, "step %zu: GEMM leading dimension too small", idx);
       if (mode == 1 && s[4] < 0)
         return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: activation gradient needs aux", idx);
+      if (mode == 2) {
+        // forward with its cotangent: dY in aux, dZ in slot 7, no accumulation or update, and
+        // dZ distinct from every slot the step reads or writes
+        if (s[4] < 0 || s[7] < 0 || a[11] != 0 || !st.payload.empty())
+          return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED,
+                      "step %zu: a forward GEMM with its cotangent needs dY and dZ slots", idx);
+        if (!v.slot_ok(s[7], false, "dZ") || !v.holds(s[7], span(M, N, ldaux), DT_F32, "dZ") ||
+            !v.writable(s[7], "dZ"))
+          return v.err;
+        for (int k = 0; k < 6; ++k)
+          if (s[k] == s[7])
+            return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: dZ aliases another operand", idx);
+        if (s[4] == s[2])  // the epilogue stores C before it reads dY
+          return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: dY aliases C", idx);
+      } else if (s[7] >= 0) {
+        return fail(SHK_HIP_STATUS_GRAPH_COMPILATION_FAILED, "step %zu: dZ slot without mode 2", idx);
+      }
       if (!st.payload.empty()) {
         const int32_t u = validate_gemm_update(v, idx, st);
         if (u == SHK_HIP_STATUS_OK)
@@ -702,6 +719,7 @@ hipError_t enqueue_step(const Step& st, const Bound& b, hipStream_t stream, doub
       p.transA = (int)a[7]; p.transB = (int)a[8];
       p.act = (int)a[9]; p.mode = (int)a[10]; p.accumulate = (int)a[11];
       p.colsum = b.get<float>(s[5]);
+      p.dz = b.get<float>(s[7]);
       if (!st.payload.empty()) {
         const OptEntry& e = *reinterpret_cast<const OptEntry*>(st.payload.data());
         shk::GemmUpdate& u = p.upd;
@@ -820,7 +838,7 @@ Access step_access(const Step& st) {
   auto W = [&](int32_t v) { if (v >= 0) x.w.push_back(v); };
   switch (rec.opcode) {
     case OP_GEMM:
-      R(sl[0]); R(sl[1]); R(sl[3]); R(sl[4]); W(sl[2]); W(sl[5]);
+      R(sl[0]); R(sl[1]); R(sl[3]); R(sl[4]); W(sl[2]); W(sl[5]); W(sl[7]);
       if (a[11]) R(sl[2]);  // accumulate
       if (!st.payload.empty()) {
         const OptEntry& e = *reinterpret_cast<const OptEntry*>(st.payload.data());

@@ -132,16 +132,25 @@ class ProgramBuilder:
     # ---- steps ----
     def gemm(self, A, B, C, M, N, K, *, trans_a=False, trans_b=False, lda=None, ldb=None,
              ldc=None, bias=None, act=None, aux=None, act_grad=False, ldaux=None,
-             accumulate=False, colsum=None) -> Step:
+             accumulate=False, colsum=None, dy=None, dz=None) -> Step:
         """C = op(A).op(B) (+bias, act) or C = act_grad(act, op(A).op(B), aux); `colsum`
-        optionally receives the column sums of the stored C (a bias gradient)."""
+        optionally receives the column sums of the stored C (a bias gradient).
+
+        With `dy` and `dz` (a forward GEMM with its cotangent), C = act(op(A).op(B) + bias) and
+        dz = act_grad(act, dy, C) (dy and dz with leading dimension ldaux); `colsum` then
+        receives the column sums of dz."""
         lda = lda if lda is not None else (M if trans_a else K)
         ldb = ldb if ldb is not None else (K if trans_b else N)
         ldc = ldc if ldc is not None else N
         ldaux = ldaux if ldaux is not None else N
-        return self._add(OP_GEMM, [A, B, C, bias, aux, colsum],
+        if (dy is None) != (dz is None):
+            raise ValueError("dy and dz go together")
+        if dy is not None and (act_grad or aux is not None or accumulate):
+            raise ValueError("a forward GEMM with its cotangent has no aux, act_grad or accumulate")
+        mode = 2 if dy is not None else (1 if act_grad else 0)
+        return self._add(OP_GEMM, [A, B, C, bias, dy if dy is not None else aux, colsum, None, dz],
                          [M, N, K, lda, ldb, ldc, ldaux, int(trans_a), int(trans_b), ACT[act],
-                          1 if act_grad else 0, 1 if accumulate else 0])
+                          mode, 1 if accumulate else 0])
 
     def gemm_update(self, A, B, M, N, K, counter, tensor, *, kind: str, trans_a=False,
                     trans_b=False, lda=None, ldb=None, lr: float, momentum=0.0, dampening=0.0,

@@ -651,7 +651,8 @@ def lower_dense_layer(batch: int, fan_in: int, fan_out: int, activation: str | N
     Y = act(X . W^T + b) for W [out, in] ("out_in", Linear's layout); returns Y, dX, dW, db.
 
     Inputs X [B,in], W, b [out], dY [B,out]; outputs Y, dX [B,in], dW (W's layout), db [out].
-    dZ = act_grad(dY, Y) is one pointwise pass; dX and dW are MFMA GEMMs; db is a column sum.
+    The forward GEMM's epilogue also forms dZ = act_grad(dY, Y) and the column sums db of dZ;
+    dX and dW are MFMA GEMMs over dZ.
     """
     from .program import PW
     pb = ProgramBuilder()
@@ -664,20 +665,20 @@ def lower_dense_layer(batch: int, fan_in: int, fan_out: int, activation: str | N
     dW = pb.output(fan_in * fan_out)
     db = pb.output(fan_out)
     in_out = weight_layout == "in_out"
-    pb.gemm(X, W, Y, batch, fan_out, fan_in, trans_b=not in_out, bias=b, act=activation)
-    dZ = pb.internal(batch * fan_out)
-    grad_op = {None: None, "relu": "relu_grad", "tanh": "tanh_grad", "sigmoid": "sigmoid_grad"}[activation]
-    if grad_op is None:
-        pb.copy(dY, dZ, batch * fan_out)
+    if activation is None:
+        # dZ = dY: the backward GEMMs read the cotangent as given
+        pb.gemm(X, W, Y, batch, fan_out, fan_in, trans_b=not in_out, bias=b)
+        dZ = dY
+        pb.colsum(dZ, db, batch, fan_out)
     else:
-        pb.pointwise(batch, fan_out, [Y, dY], [dZ],
-                     [("load", 0, 0, 0, 0, 0.0), ("load", 1, 1, 0, 0, 0.0),
-                      (grad_op, 2, 0, 1, 0, 0.0), ("store", 0, 2, 0, 0, 0.0)])
+        # the forward GEMM's epilogue also forms dZ = act_grad(dY, Y) and db = SUM_TO_SHAPE(dZ)
+        dZ = pb.internal(batch * fan_out)
+        pb.gemm(X, W, Y, batch, fan_out, fan_in, trans_b=not in_out, bias=b, act=activation,
+                dy=dY, dz=dZ, colsum=db)
     if in_out:
         pb.gemm(dZ, W, dX, batch, fan_in, fan_out, trans_b=True)        # dX = dZ . W^T
         pb.gemm(X, dZ, dW, fan_in, fan_out, batch, trans_a=True)        # dW = X^T . dZ
     else:
         pb.gemm(dZ, W, dX, batch, fan_in, fan_out)                      # dX = dZ . W
         pb.gemm(dZ, X, dW, fan_out, fan_in, batch, trans_a=True)        # dW = dZ^T . X
-    pb.colsum(dZ, db, batch, fan_out)
     return pb, (Y, dX, dW, db)

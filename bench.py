@@ -170,6 +170,34 @@ def probe() -> int:
     return 0
 
 
+def c3_line(ctx, rng, one_stream: bool = False) -> dict:
+    """C3: 784 -> 1024 -> 1024 -> 10 classifier, softmax-CE, Adam, batch 1024: the configuration's
+    50-step run (objective after its first and last step; it also captures the step's graphs),
+    then 200 more steps timed. one_stream: the program's steps on one stream (for kernel traces
+    whose per-kernel times are not shared with concurrent work)."""
+    from synaptik_amd.training import Adam, HipTrainingSession, MlpSpec, init_parameters
+    spec = MlpSpec.chain([784, 1024, 1024, 10], hidden="relu", loss="ce")
+    Ws, bs = init_parameters(spec, 0, "he_normal")
+    sess = HipTrainingSession.open(ctx, spec, Ws, bs, Adam(1e-3, 0.9, 0.999, 1e-8), 1024)
+    if one_stream:
+        sess.program.set_concurrent(False)
+    xb = ctx.upload(rng.uniform(0, 1, (1024, 784)).astype(np.float32))
+    yb = ctx.upload(rng.integers(0, 10, 1024).astype(np.int64))
+    sess.run_resident(xb, yb)
+    first = float(sess.objective())
+    for _ in range(49):
+        sess.run_resident(xb, yb)
+    last = float(sess.objective())
+    t0 = time.perf_counter()
+    for _ in range(200):
+        sess.run_resident(xb, yb)
+    wall = time.perf_counter() - t0
+    sess.close()
+    return {"samples_per_s": round(200 * 1024 / wall, 1), "ms_per_step": round(wall / 200 * 1e3, 4),
+            "objective_step1": first, "objective_step50": last, "timed": "steps 51-250",
+            "streams": 1 if one_stream else 2}
+
+
 def secondary(ctx, reps: int = 5, cpu: bool = True) -> dict:
     """The other benchmark configurations, measured on the same context (not the headline value)."""
     from synaptik_amd.native import HipProgram
@@ -256,28 +284,7 @@ def secondary(ctx, reps: int = 5, cpu: bool = True) -> dict:
                              "device_ms_profiled": round(dev, 4),
                              "steps_ms_profiled": [round(v / runs, 4) for v in t]}
     prog.close()
-    # C3: 784 -> 1024 -> 1024 -> 10 classifier, softmax-CE, Adam, batch 1024
-    spec = MlpSpec.chain([784, 1024, 1024, 10], hidden="relu", loss="ce")
-    Ws, bs = init_parameters(spec, 0, "he_normal")
-    sess = HipTrainingSession.open(ctx, spec, Ws, bs, Adam(1e-3, 0.9, 0.999, 1e-8), 1024)
-    xb = ctx.upload(rng.uniform(0, 1, (1024, 784)).astype(np.float32))
-    yb = ctx.upload(rng.integers(0, 10, 1024).astype(np.int64))
-    # the config's 50-step run (objective after its first and its last step; it also captures
-    # the step's graphs), then 200 more steps timed
-    sess.run_resident(xb, yb)
-    first = float(sess.objective())
-    for _ in range(49):
-        sess.run_resident(xb, yb)
-    last = float(sess.objective())
-    t0 = time.perf_counter()
-    for _ in range(200):
-        sess.run_resident(xb, yb)
-    wall = time.perf_counter() - t0
-    out["c3_classifier_adam"] = {"samples_per_s": round(200 * 1024 / wall, 1),
-                                 "ms_per_step": round(wall / 200 * 1e3, 4),
-                                 "objective_step1": first, "objective_step50": last,
-                                 "timed": "steps 51-250"}
-    sess.close()
+    out["c3_classifier_adam"] = c3_line(ctx, rng)
     # C1: 16 -> 64 -> 1 tanh MLP, MSE, SGD 0.01, batch 256 (builder weights, seed 0): the
     # 20-step run, launch-bound; the first run also captures the step's graph
     spec = MlpSpec.chain([16, 64, 1], hidden="tanh", loss="mse")
@@ -424,6 +431,10 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true", help="skip the C2/C3/C5 lines")
     ap.add_argument("--probe", action="store_true",
                     help="counter probe: 3 launches each of one 4096^3 NT GEMM and a 256 MiB copy")
+    ap.add_argument("--c3-only", action="store_true",
+                    help="only the C3 line (for kernel profiles of the classifier step)")
+    ap.add_argument("--one-stream", action="store_true",
+                    help="with --c3-only: run the step's program on one stream")
     ap.add_argument("--secondary-only", action="store_true",
                     help="only the C2/C3/C5 and publication lines, without CPU baselines "
                          "(for kernel profiles)")
@@ -437,6 +448,11 @@ def main() -> int:
 
     from synaptik_amd.native import HipContext
     ctx = HipContext(0)
+    if args.c3_only:
+        print(json.dumps({"c3_classifier_adam": c3_line(ctx, np.random.default_rng(7),
+                                                        args.one_stream)}), flush=True)
+        ctx.close()
+        return 0
     if args.secondary_only:
         print(json.dumps({"secondary": secondary(ctx, cpu=False)}), flush=True)
         ctx.close()

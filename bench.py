@@ -198,6 +198,45 @@ def c3_line(ctx, rng, one_stream: bool = False) -> dict:
             "streams": 1 if one_stream else 2}
 
 
+def gemm_layouts(ctx, reps: int = 20, warmup: int = 10) -> dict:
+    """Plain GEMMs (no epilogue work beyond the store) in the four operand layouts, per shape:
+    TFLOP/s from HIP events around each launch. The four programs are warmed up and then run in
+    rotation, so that a clock or thermal drift falls on every layout alike. The training step's
+    dW launches are TN with a fused optimizer update; this isolates the layout itself."""
+    from synaptik_amd.native import HipProgram
+    from synaptik_amd.program import ProgramBuilder
+    rng = np.random.default_rng(0)
+    out = {}
+    layouts = (("NT", (0, 1)), ("NN", (0, 0)), ("TN", (1, 0)), ("TT", (1, 1)))
+    for (M, N, K) in ((4096, 4096, 4096), (8192, 1024, 1024), (1024, 1024, 1024)):
+        A = ctx.upload(rng.standard_normal(M * K, dtype=np.float32))
+        B = ctx.upload(rng.standard_normal(K * N, dtype=np.float32))
+        C = ctx.buffer(M * N * 4)
+        progs = {}
+        for name, (ta, tb) in layouts:
+            pb = ProgramBuilder()
+            a, b, c = pb.input(M * K), pb.input(K * N), pb.output(M * N)
+            pb.gemm(a, b, c, M, N, K, trans_a=bool(ta), trans_b=bool(tb))
+            progs[name] = HipProgram(ctx, pb.image())
+        for _ in range(warmup):
+            for prog in progs.values():
+                prog.run([A, B], [C])
+        for prog in progs.values():
+            prog.set_profiling(True)
+        for _ in range(reps):
+            for prog in progs.values():
+                prog.run([A, B], [C])
+        row = {}
+        for name, prog in progs.items():
+            t, runs = prog.step_times()
+            row[name] = round(2 * M * N * K / (t[0] / runs * 1e-3) / 1e12, 2)
+            prog.close()
+        for x in (A, B, C):
+            x.close()
+        out[f"{M}x{N}x{K}"] = row
+    return out
+
+
 def secondary(ctx, reps: int = 5, cpu: bool = True) -> dict:
     """The other benchmark configurations, measured on the same context (not the headline value)."""
     from synaptik_amd.native import HipProgram
@@ -431,6 +470,8 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true", help="skip the C2/C3/C5 lines")
     ap.add_argument("--probe", action="store_true",
                     help="counter probe: 3 launches each of one 4096^3 NT GEMM and a 256 MiB copy")
+    ap.add_argument("--gemm-layouts", action="store_true",
+                    help="plain GEMM TFLOP/s in the NT / NN / TN / TT layouts at three shapes")
     ap.add_argument("--c3-only", action="store_true",
                     help="only the C3 line (for kernel profiles of the classifier step)")
     ap.add_argument("--one-stream", action="store_true",
@@ -448,6 +489,10 @@ def main() -> int:
 
     from synaptik_amd.native import HipContext
     ctx = HipContext(0)
+    if args.gemm_layouts:
+        print(json.dumps({"gemm_layouts_TFLOPs": gemm_layouts(ctx)}), flush=True)
+        ctx.close()
+        return 0
     if args.c3_only:
         print(json.dumps({"c3_classifier_adam": c3_line(ctx, np.random.default_rng(7),
                                                         args.one_stream)}), flush=True)

@@ -89,7 +89,8 @@ struct V2Loader {
                                         int k_left) const {
     const uint32_t dst =
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)lds + I * 4096u + wdst;
-    if (!TAIL || (vrow[I] < rows_left && vk[I] < k_left)) {
+    // a whole tile row-range and a whole k-tile (uniform) need no per-lane bounds
+    if (!TAIL || (rows_left >= BT && k_left >= V2_BK) || (vrow[I] < rows_left && vk[I] < k_left)) {
       asm volatile("global_load_lds_dwordx4 %0, %1"
                    :
                    : "v"(voff[I]), "s"(tile), "{m0}"(dst)
@@ -306,11 +307,11 @@ gemm_f32_v2(GemmParams p) {
   copy_all(a_tile, b_tile, As0, Bs0, (int)k_len);
   if (nk > 1) {
     copy_all(a_tile + a_step, b_tile + b_step, As1, Bs1, (int)(k_len - V2_BK));
-    if constexpr (TAIL) {
-      // lanes that stored zeros have fewer copies in flight: wait for all of them
+    // vmcnt(2 NI) says the first k-tile's copies have landed only when every lane issued all
+    // of its copies for both k-tiles: otherwise (lanes that stored zeros) wait for everything
+    if (TAIL && !(rows_a == BT && rows_b == BT && k_len >= 2 * V2_BK)) {
       v2_wait_all();
     } else {
-      // vmcnt(2 NI): the first k-tile's copies have landed
       if constexpr (NI == 4) __builtin_amdgcn_s_waitcnt(0x0F78);
       else __builtin_amdgcn_s_waitcnt(0x0F74);
     }

@@ -234,9 +234,10 @@ int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K, bool colsum) {
   if (colsum && K >= 2 && K <= 16)  // small-K kernel: one binary64 partial row per row block
     floats = std::max<int64_t>(floats, 2 * small_k_row_blocks(M, N) * N);
   if (colsum) {
-    // the fused path writes ceil(M/BM) * BM/WM binary64 rows, at most (M + 255) / 32 for every
-    // configuration (BM <= 256, WM >= 32); the split path's separate pass needs far fewer
-    floats = std::max<int64_t>(floats, 2 * ((M + 255) / 32) * N);
+    // the fused path writes ceil(M/BM) * BM/WM binary64 rows (two K groups of 64x64 tiles:
+    // ceil(M/64) * 4), at most (M + 255) / 16 for every configuration; the split path's separate
+    // pass needs far fewer
+    floats = std::max<int64_t>(floats, 2 * ((M + 255) / 16) * N);
   }
   return floats;
 }

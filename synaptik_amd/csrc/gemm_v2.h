@@ -396,36 +396,6 @@ gemm_f32_v2(GemmParams p) {
   }
   v2_wait_all();
   v2_barrier();  // every wave has finished reading its fragments: the stages are free
-  if constexpr (KS == 2) {
-    // group 1 -> group 0: accumulator (block I, J, register R) of wave w, lane l at
-    // ((I NB + J) 4 + R) 64 + l of a 4 NB^2 x 64 slab in group 1's (free) stages: waves 0, 1 in
-    // its A0 stage, waves 2, 3 in its B0 stage (two slabs per stage)
-    static_assert(2 * 4 * NB * NB * 64 <= TILEF, "exchange slabs must fit group 1's stages");
-    float* xchg = (wave < 2 ? As0g : Bs0g) + TILEF + (wave & 1) * (4 * NB * NB * 64);
-    if (kgroup == 1) {
-      static_for<NB>([&](auto i) {
-        static_for<NB>([&](auto j) {
-          constexpr int I = decltype(i)::value, J = decltype(j)::value;
-          static_for<4>([&](auto r) {
-            constexpr int R = decltype(r)::value;
-            xchg[((I * NB + J) * 4 + R) * 64 + lane] = acc[I][J][R];
-          });
-        });
-      });
-      __builtin_amdgcn_s_waitcnt(0xC07F);
-    }
-    v2_barrier();
-    if (kgroup == 1) return;
-    static_for<NB>([&](auto i) {
-      static_for<NB>([&](auto j) {
-        constexpr int I = decltype(i)::value, J = decltype(j)::value;
-        static_for<4>([&](auto r) {
-          constexpr int R = decltype(r)::value;
-          acc[I][J][R] = acc[I][J][R] + xchg[((I * NB + J) * 4 + R) * 64 + lane];
-        });
-      });
-    });
-  }
   constexpr int ECPR = Cfg::ECPR, RSTEP = 64 / ECPR, PER_ARRAY = TILEF / (WT * WT);
   const int arr = wave / PER_ARRAY;
   float* stage = (arr == 0 ? As0 : arr == 1 ? Bs0 : arr == 2 ? As1 : Bs1) +
@@ -459,11 +429,27 @@ gemm_f32_v2(GemmParams p) {
     });
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are complete
+  // KS = 2: each group has staged its partial tile in its own stages; after the barrier group h
+  // stores rows [h WT / 2, (h + 1) WT / 2) of every wave tile, each value the sum of the two
+  // partial tiles in a fixed order (group 0's + group 1's), so both groups share the epilogue.
+  if constexpr (KS == 2) v2_barrier();
+  const float* stage0 = (arr == 0 ? As0g : arr == 1 ? Bs0g : arr == 2 ? As1g : Bs1g) +
+                        (wave % PER_ARRAY) * (WT * WT);
   const int q = lane % ECPR, rg = lane / ECPR;
   auto tile_row = [&](int t) -> floatx4 {
     const int row = rg + RSTEP * t;
-    return *reinterpret_cast<const floatx4*>(stage + row * WT + ((q ^ (row % ECPR)) << 2));
+    const int off = row * WT + ((q ^ (row % ECPR)) << 2);
+    if constexpr (KS == 1) {
+      return *reinterpret_cast<const floatx4*>(stage + off);
+    } else {
+      const floatx4 v0 = *reinterpret_cast<const floatx4*>(stage0 + off);
+      const floatx4 v1 = *reinterpret_cast<const floatx4*>(stage0 + TILEF + off);
+      return floatx4{v0[0] + v1[0], v0[1] + v1[1], v0[2] + v1[2], v0[3] + v1[3]};
+    }
   };
+  static_assert(KS == 1 || (WT / RSTEP) % KS == 0, "row steps split evenly between the groups");
+  constexpr int TSTEPS = WT / RSTEP / KS;  // row steps per group
+  const int tfirst = kgroup * TSTEPS;
   const int64_t row_e = m0 + wm * WT + rg, col_e = n0 + wn * WT + 4 * q;
   const bool col_ok = !TAIL || col_e < p.N;  // N is a multiple of 4: whole segments
   // The loops below are compiled once per optimizer kind / (mode, activation, accumulate): a
@@ -474,7 +460,7 @@ gemm_f32_v2(GemmParams p) {
     bool ok = uc.k.ok;
     auto update_rows = [&](auto kindc) {
       constexpr bool SGD = decltype(kindc)::value == 0;
-      for (int t = 0; t < WT / RSTEP; ++t) {
+      for (int t = tfirst; t < tfirst + TSTEPS; ++t) {
         const int64_t row = row_e + RSTEP * t;
         if (TAIL && (!col_ok || row >= p.M)) continue;
         const int64_t e = row * p.N + col_e;
@@ -509,7 +495,7 @@ gemm_f32_v2(GemmParams p) {
   auto store_rows = [&](auto modec, auto actc, auto accc) {
     constexpr int MODE = decltype(modec)::value, ACT = decltype(actc)::value;
     constexpr bool ACC = decltype(accc)::value;
-    for (int t = 0; t < WT / RSTEP; ++t) {
+    for (int t = tfirst; t < tfirst + TSTEPS; ++t) {
       const int64_t row = row_e + RSTEP * t;
       if (TAIL && (!col_ok || row >= p.M)) continue;
       floatx4 v = tile_row(t);
@@ -563,7 +549,8 @@ gemm_f32_v2(GemmParams p) {
       for (int o = ECPR; o < 64; o <<= 1) cs[C] += __shfl_xor(cs[C], o, 64);
     });
     if (rg == 0 && col_ok) {
-      double* dst = p.colsum_partial + ((int64_t)tm * 2 + wm) * p.N + col_e;
+      // one partial row per wave row and K group
+      double* dst = p.colsum_partial + (((int64_t)tm * 2 + wm) * KS + kgroup) * p.N + col_e;
       static_for<4>([&](auto c) { dst[decltype(c)::value] = cs[decltype(c)::value]; });
     }
   }
@@ -637,6 +624,7 @@ hipError_t launch_v2_bt(const GemmParams& p, hipStream_t s) {
   const int64_t span = p.kchunk > 0 ? p.kchunk : p.K;
   if constexpr (BT == 64) {
     if (v2_split_in_group(p, BT)) {
+      g_colsum_rows = ((p.M + BT - 1) / BT) * 4;  // per wave row and K group
       // both groups whole k-tiles only when K is a multiple of 2 BK
       const bool tail = p.M % BT != 0 || p.N % BT != 0 || p.K % (2 * V2_BK) != 0;
       if (tail)

@@ -225,6 +225,10 @@ struct Lease {
   double* scratch_side = nullptr;  // ... of the side stream's steps (two-stream plan)
   uint32_t* host_status = nullptr; // pinned; written by the run's status publication kernel
   hipEvent_t done = nullptr;       // end of the run
+  // Private streams the lease's graphs are captured on (then launched on the context stream):
+  // another thread may synchronize the shared streams at any time, which would invalidate a
+  // capture running on them.
+  hipStream_t cap0 = nullptr, cap1 = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
   std::vector<hipEvent_t> step_done;  // per step the other stream waits for
   std::vector<hipEvent_t> events;     // per-step timing (profiled runs), created on first use
@@ -941,7 +945,7 @@ void plan_streams(Program* pr) {
 // performed by the publication kernel: the commit reads the status word, so every step that can
 // flag it precedes it, and nothing follows.
 hipError_t enqueue_steps(const Program& pr, Lease& ls, const Bound& b, hipStream_t s0,
-                         bool two_streams, bool profile) {
+                         bool two_streams, bool profile, hipStream_t side = nullptr) {
   hipError_t e = hipSuccess;
   const size_t n = pr.steps.size();
   int64_t* commit = nullptr;
@@ -958,7 +962,7 @@ hipError_t enqueue_steps(const Program& pr, Lease& ls, const Bound& b, hipStream
     if (profile && (e = hipEventRecord(ls.events[n], s0)) != hipSuccess) return e;
     return shk::launch_status_publish(ls.status, ls.host_status, commit, s0);
   }
-  hipStream_t s1 = pr.ctx->side_stream;
+  hipStream_t s1 = side != nullptr ? side : pr.ctx->side_stream;
   if ((e = hipEventRecord(ls.fork, s0)) != hipSuccess ||
       (e = hipStreamWaitEvent(s1, ls.fork, 0)) != hipSuccess)
     return e;
@@ -985,6 +989,8 @@ void destroy_lease(Lease* ls) {
   for (hipEvent_t e : ls->step_done)
     if (e != nullptr) (void)hipEventDestroy(e);
   if (ls->done != nullptr) (void)hipEventDestroy(ls->done);
+  if (ls->cap0 != nullptr) (void)hipStreamDestroy(ls->cap0);
+  if (ls->cap1 != nullptr) (void)hipStreamDestroy(ls->cap1);
   if (ls->fork != nullptr) (void)hipEventDestroy(ls->fork);
   if (ls->join != nullptr) (void)hipEventDestroy(ls->join);
   if (ls->host_status != nullptr) (void)hipHostFree(ls->host_status);
@@ -1015,6 +1021,15 @@ int32_t create_lease(const Program& pr, Lease** out) {
   }
   bool ok = hipEventCreateWithFlags(&ls->done, hipEventDisableTiming) == hipSuccess;
   if (!ok) ls->done = nullptr;
+  if (ok && hipStreamCreateWithFlags(&ls->cap0, hipStreamNonBlocking) != hipSuccess) {
+    ls->cap0 = nullptr;
+    ok = false;
+  }
+  if (ok && pr.side_steps > 0 &&
+      hipStreamCreateWithFlags(&ls->cap1, hipStreamNonBlocking) != hipSuccess) {
+    ls->cap1 = nullptr;
+    ok = false;
+  }
   ls->status = static_cast<uint32_t*>(ls->arena);
   ls->scratch = reinterpret_cast<double*>(static_cast<char*>(ls->arena) + pr.scratch_off);
   if (ok && pr.side_steps > 0) {
@@ -2043,10 +2058,12 @@ int32_t run_program(void* program, uint32_t input_count, void* const* inputs, ui
         // capture: every step + the status publication (kernels only, no memset or copy node)
         hipGraph_t graph = nullptr;
         hipGraphExec_t exec = nullptr;
-        bool ok = hipStreamBeginCapture(stream, hipStreamCaptureModeRelaxed) == hipSuccess;
+        // captured on the lease's private streams, launched on the context stream below
+        bool ok = hipStreamBeginCapture(ls->cap0, hipStreamCaptureModeRelaxed) == hipSuccess;
         if (ok) {
-          const bool steps_ok = enqueue_steps(*pr, *ls, b, stream, two_streams, false) == hipSuccess;
-          const bool ended = hipStreamEndCapture(stream, &graph) == hipSuccess;
+          const bool steps_ok =
+              enqueue_steps(*pr, *ls, b, ls->cap0, two_streams, false, ls->cap1) == hipSuccess;
+          const bool ended = hipStreamEndCapture(ls->cap0, &graph) == hipSuccess;
           ok = steps_ok && ended && graph != nullptr &&
                hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess;
           if (graph != nullptr) (void)hipGraphDestroy(graph);

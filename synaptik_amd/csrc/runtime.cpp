@@ -906,6 +906,15 @@ bool concurrency_enabled() {
 // Two-stream list schedule: step j goes beside the main chain (stream 1) when it does not
 // depend on the step currently at the tail of stream 0; a step waits (event) for every earlier
 // step on the other stream it depends on. Steps on one stream keep program order.
+// A GEMM with at least 2^28 multiply-adds: enough tiles to occupy every CU on its own.
+bool large_gemm(const Step& st) {
+  if (st.rec.opcode != OP_GEMM) return false;
+  const int64_t* a = st.rec.iarg;
+  if (a[0] <= 0 || a[1] <= 0 || a[2] <= 0) return false;
+  const double macs = (double)a[0] * (double)a[1] * (double)a[2];
+  return macs >= (double)(1ll << 28);
+}
+
 void plan_streams(Program* pr) {
   const size_t n = pr->steps.size();
   pr->stream_of.assign(n, 0);
@@ -922,7 +931,11 @@ void plan_streams(Program* pr) {
       if (accesses_conflict(acc[i], acc[j])) deps.push_back((uint32_t)i);
     bool on_tail0 = tail0 < 0;
     for (uint32_t i : deps) on_tail0 |= (int64_t)i == tail0;
-    const uint8_t sj = on_tail0 ? 0 : 1;
+    // A large GEMM stays on the context stream even when it could run beside the chain: two
+    // of them side by side take longer than one after the other (measured on MI355X: 1024^3 NN
+    // and TN GEMMs, 46 us in sequence, 72 us on two streams), so the side stream carries only
+    // the small steps that fill the gaps.
+    const uint8_t sj = (on_tail0 || large_gemm(pr->steps[j])) ? 0 : 1;
     pr->stream_of[j] = sj;
     if (sj == 0) tail0 = (int64_t)j;
     // stream order covers same-stream dependencies and the other stream's earlier ones

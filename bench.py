@@ -308,7 +308,8 @@ def secondary(ctx, reps: int = 5, cpu: bool = True) -> dict:
     obs = [ctx.buffer(s.nbytes) for s in outs]
     for _ in range(5):
         prog.run(ins, obs)
-    # replayed graph with the two-stream schedule (dX beside dW), 100 synchronous calls
+    # the runtime's default launch mode (direct launches: every step is a large GEMM) with the
+    # two-stream schedule, 100 synchronous calls
     t0 = time.perf_counter()
     for _ in range(100):
         prog.run(ins, obs)
@@ -320,6 +321,7 @@ def secondary(ctx, reps: int = 5, cpu: bool = True) -> dict:
     t, runs = prog.step_times()
     dev = sum(t) / runs
     out["c2_fused_layer"] = {"ms": round(wall, 4), "TFLOPs": round(3 * 2 * B * I * O / wall / 1e9, 1),
+                             "graph_replay": prog.graph_mode(),
                              "device_ms_profiled": round(dev, 4),
                              "steps_ms_profiled": [round(v / runs, 4) for v in t]}
     prog.close()

@@ -217,10 +217,14 @@ int32_t shk_hip_program_set_profiling(void* program, int32_t enabled);
 int32_t shk_hip_program_step_times(void* program, double* out_milliseconds, uint32_t capacity,
                                    uint64_t* out_runs);
 int32_t shk_hip_program_step_count(void* program, uint32_t* out_steps);
-/* HIP-graph replay of the whole step sequence (default on; SHK_HIP_GRAPHS=0 turns the default
- * off): each distinct set of bound buffers is captured once and replayed with one launch.
- * Profiled runs always launch step by step. */
+/* HIP-graph replay of the whole step sequence: each distinct set of bound buffers is captured
+ * once and replayed with one launch. The default is on, except for a program whose every step
+ * is a GEMM large enough to occupy the device (at least 2^28 multiply-adds): there the launches
+ * are hidden behind the previous kernel anyway and replay only adds per-node cost.
+ * SHK_HIP_GRAPHS=0 turns the default off. Profiled runs always launch step by step. */
 int32_t shk_hip_program_set_graph_mode(void* program, int32_t enabled);
+/* The current graph-replay setting (HIP addition). */
+int32_t shk_hip_program_graph_mode(void* program, int32_t* out_enabled);
 
 #ifdef __cplusplus
 }

@@ -73,6 +73,7 @@ EXPORTED_SYMBOLS = (
     "shk_hip_program_step_times",
     "shk_hip_program_step_count",
     "shk_hip_program_set_graph_mode",
+    "shk_hip_program_graph_mode",
 )
 
 
@@ -166,6 +167,7 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
                                                  ctypes.POINTER(u64)]),
             "shk_hip_program_step_count": (i32, [vp, ctypes.POINTER(u32)]),
             "shk_hip_program_set_graph_mode": (i32, [vp, i32]),
+            "shk_hip_program_graph_mode": (i32, [vp, ctypes.POINTER(i32)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -430,6 +432,11 @@ class HipProgram:
 
     def set_graph_mode(self, enabled: bool) -> None:
         check(self.lib, self.lib.shk_hip_program_set_graph_mode(self.handle, 1 if enabled else 0))
+
+    def graph_mode(self) -> bool:
+        v = ctypes.c_int32(0)
+        check(self.lib, self.lib.shk_hip_program_graph_mode(self.handle, ctypes.byref(v)))
+        return v.value != 0
 
     def set_profiling(self, enabled: bool) -> None:
         check(self.lib, self.lib.shk_hip_program_set_profiling(self.handle, 1 if enabled else 0))

@@ -63,3 +63,32 @@ def test_graph_replay_accumulation_modes(ctx):
     a, b = sess[0].state(), sess[1].state()
     for u, v in zip(a.weights + a.biases + a.first, b.weights + b.biases + b.first):
         assert np.array_equal(u, v)
+
+
+def test_default_launch_mode_follows_the_program(ctx):
+    """Programs of large GEMMs only launch step by step by default; any other program replays a
+    graph. Either mode gives identical results."""
+    from synaptik_amd.training import lower_dense_layer
+    B, I, O = 1024, 512, 512  # every GEMM 2^28 multiply-adds
+    pb, outs = lower_dense_layer(B, I, O, "relu", "in_out")
+    progs = [HipProgram(ctx, pb.image()) for _ in range(2)]
+    assert not progs[0].graph_mode()
+    progs[1].set_graph_mode(True)
+    assert progs[1].graph_mode()
+    rng = np.random.default_rng(8)
+    ins = [ctx.upload(rng.standard_normal(n, dtype=np.float32)) for n in (B * I, I * O, O, B * O)]
+    res = []
+    for p in progs:
+        obs = [ctx.buffer(s.nbytes) for s in outs]
+        for _ in range(3):
+            p.run(ins, obs)
+        res.append([o.download() for o in obs])
+        p.close()
+    for u, v in zip(*res):
+        assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
+    small, _ = lower_dense_layer(64, 32, 32, "relu", "in_out")
+    p = HipProgram(ctx, small.image())
+    assert p.graph_mode()
+    p.set_graph_mode(False)
+    assert not p.graph_mode()
+    p.close()

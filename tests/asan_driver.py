@@ -107,6 +107,16 @@ def main():
     assert lib.shk_hip_program_run(junk, 0, None, 0, None) == 1
     assert lib.shk_hip_program_run_static(junk, 0, None, 0, None) == 1
     assert lib.shk_hip_program_validate(None, 0, None) == 1
+    for fn in ("shk_hip_program_set_graph_mode", "shk_hip_program_set_concurrent",
+               "shk_hip_program_set_profiling"):
+        assert getattr(lib, fn)(None, 1) == 1 and getattr(lib, fn)(junk, 0) == 1
+    i32, u32, u64 = ctypes.c_int32(5), ctypes.c_uint32(5), ctypes.c_uint64(5)
+    assert lib.shk_hip_program_graph_mode(junk, ctypes.byref(i32)) == 1 and i32.value == 0
+    assert lib.shk_hip_program_graph_mode(junk, None) == 1
+    for fn in ("shk_hip_program_side_steps", "shk_hip_program_step_count",
+               "shk_hip_program_lease_count"):
+        assert getattr(lib, fn)(junk, ctypes.byref(u32)) == 1
+    assert lib.shk_hip_program_arena_bytes(junk, ctypes.byref(u64)) == 1
     msg = ctypes.create_string_buffer(64)
     assert lib.shk_hip_last_error(msg, 64) == 0
     assert lib.shk_hip_last_error(None, 0) == 1

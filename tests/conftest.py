@@ -9,6 +9,16 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 
+# The runtime's environment switches (SHK_HIP_CONCURRENT=0, SHK_HIP_GRAPHS=0) turn off features
+# whose defaults some tests assert; those tests skip under them, the rest run unchanged.
+TWO_STREAMS_OFF = os.environ.get("SHK_HIP_CONCURRENT", "")[:1] == "0"
+GRAPHS_OFF = os.environ.get("SHK_HIP_GRAPHS", "")[:1] == "0"
+needs_two_streams = pytest.mark.skipif(TWO_STREAMS_OFF, reason="SHK_HIP_CONCURRENT=0 turns the "
+                                                                "two-stream schedule off")
+needs_graph_default = pytest.mark.skipif(GRAPHS_OFF, reason="SHK_HIP_GRAPHS=0 turns the graph "
+                                                             "default off")
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) and libsynaptik_hip.so")
 

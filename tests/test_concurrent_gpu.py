@@ -8,6 +8,7 @@ import pytest
 from synaptik_amd.native import HipProgram
 from synaptik_amd.training import (Adam, HipTrainingSession, MlpSpec, Sgd, init_parameters,
                                    lower_dense_layer)
+from tests.conftest import needs_two_streams
 
 pytestmark = pytest.mark.gpu
 
@@ -16,6 +17,7 @@ def _bits(st):
     return [a.view(np.uint32).copy() for a in st.weights + st.biases + st.first + st.second]
 
 
+@needs_two_streams
 @pytest.mark.parametrize("graphs", [True, False])
 @pytest.mark.parametrize("dims,loss,opt", [
     ([784, 1024, 1024, 10], "ce", Adam(1e-3)),

@@ -7,6 +7,7 @@ import pytest
 from synaptik_amd.native import HipProgram
 from synaptik_amd.program import ProgramBuilder
 from synaptik_amd.training import Adam, GradientMode, HipTrainingSession, MlpSpec, Sgd, init_parameters
+from tests.conftest import needs_graph_default
 
 pytestmark = pytest.mark.gpu
 
@@ -65,6 +66,7 @@ def test_graph_replay_accumulation_modes(ctx):
         assert np.array_equal(u, v)
 
 
+@needs_graph_default
 def test_default_launch_mode_follows_the_program(ctx):
     """Programs of large GEMMs only launch step by step by default; any other program replays a
     graph. Either mode gives identical results."""

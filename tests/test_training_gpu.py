@@ -12,6 +12,7 @@ from oracle import oracle
 from synaptik_amd.native import HipArithmeticError, HipIndexError
 from synaptik_amd.training import (Adam, AdamW, Dense, HipTrainingSession, MlpSpec, Sgd,
                                    init_parameters)
+from tests.conftest import needs_two_streams
 
 pytestmark = pytest.mark.gpu
 
@@ -187,6 +188,7 @@ def test_state_restore_replays_bit_exactly(ctx):
     sess.close()
 
 
+@needs_two_streams
 def test_failed_two_stream_steps_leave_no_trace(ctx):
     """A classifier step whose program runs on two streams (replayed graph; the step commit is
     performed by the run's last launch) fails on an out-of-range label, then succeeds; two such

@@ -241,9 +241,20 @@ gemm_f32_v2(GemmParams p) {
                         : v2_mnmaj_off(4 * g, wn * WT + NB * l16, Cfg::CPR);
     }
   }
-  // wave sub-tile row of accumulator register R of block I, column of block J (lane column l16)
-  auto v2_row = [&](int I, int R) { return KA ? 16 * I + 4 * g + R : NB * (4 * g + R) + I; };
-  auto v2_col = [&](int J) { return KB ? 16 * J + l16 : NB * l16 + J; };
+  // Wave sub-tile row and column of accumulator register R of block (I, J). The MFMA's output
+  // lane holds four consecutive rows (4g + R) of one column (l16) of its 16 x 16 block. With a
+  // K-contiguous B the operands go into the MFMA swapped (it computes the block's transpose:
+  // products and sums are the same), so that a lane holds four consecutive columns of one row
+  // instead and the epilogue stages them with one 16-byte LDS write; an M/N-contiguous B already
+  // gives a lane NB adjacent columns through its interleaved blocks.
+  auto v2_row = [&](int I, int R) {
+    if constexpr (KB) return KA ? 16 * I + l16 : NB * l16 + I;
+    else return KA ? 16 * I + 4 * g + R : NB * (4 * g + R) + I;
+  };
+  auto v2_col = [&](int J, int R) {
+    if constexpr (KB) return 16 * J + 4 * g + R;
+    else return NB * l16 + J;
+  };
 
   floatx4 acc[NB][NB];
   static_for<NB>([&](auto i) {
@@ -253,7 +264,7 @@ gemm_f32_v2(GemmParams p) {
   });
 
   // 4 NB^2 MFMAs of one half-tile in NG groups of 8 (MFMA n: s = n / NB^2, block
-  // i = (n % NB^2) / NB, j = n % NB); after each group, side(q) issues that group's share of the
+  // i = (n % NB^2) / NB, j = n % NB, or i and j exchanged for a K-contiguous B); after each group, side(q) issues that group's share of the
   // LDS reads and copies. The scheduling barriers keep this order: reads and copies spread over
   // the MFMA stream instead of stalling it in one place.
   auto mfma_half = [&](const V2Frag<KA, BT>& fa, const V2Frag<KB, BT>& fb, auto side) {
@@ -261,9 +272,16 @@ gemm_f32_v2(GemmParams p) {
       constexpr int Q = decltype(q)::value;
       static_for<8>([&](auto u) {
         constexpr int N = 8 * Q + decltype(u)::value;
-        constexpr int S = N / (NB * NB), I = (N % (NB * NB)) / NB, J = N % NB;
-        acc[I][J] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa.f[I][S], fb.f[J][S], acc[I][J], 0, 0,
-                                                        0);
+        // (with the operands swapped, consecutive MFMAs share their first operand)
+        constexpr int S = N / (NB * NB);
+        constexpr int I = KB ? N % NB : (N % (NB * NB)) / NB;
+        constexpr int J = KB ? (N % (NB * NB)) / NB : N % NB;
+        if constexpr (KB)
+          acc[I][J] = __builtin_amdgcn_mfma_f32_16x16x4f32(fb.f[J][S], fa.f[I][S], acc[I][J], 0,
+                                                          0, 0);
+        else
+          acc[I][J] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa.f[I][S], fb.f[J][S], acc[I][J], 0,
+                                                          0, 0);
       });
       __builtin_amdgcn_sched_barrier(0);
       side(q);
@@ -384,10 +402,10 @@ gemm_f32_v2(GemmParams p) {
     static_for<NB>([&](auto i) {
       static_for<NB>([&](auto j) {
         constexpr int I = decltype(i)::value, J = decltype(j)::value;
-        const int64_t col = n0 + wn * WT + v2_col(J);
         static_for<4>([&](auto r) {
           constexpr int R = decltype(r)::value;
           const int64_t row = m0 + wm * WT + v2_row(I, R);
+          const int64_t col = n0 + wn * WT + v2_col(J, R);
           if (!TAIL || (row < p.M && col < p.N)) part[row * p.N + col] = acc[I][J][R];
         });
       });
@@ -401,14 +419,13 @@ gemm_f32_v2(GemmParams p) {
   float* stage = (arr == 0 ? As0 : arr == 1 ? Bs0 : arr == 2 ? As1 : Bs1) +
                  (wave % PER_ARRAY) * (WT * WT);
   if constexpr (KB) {
+    // the four registers of block (I, J) are columns 16 J + 4g .. + 3 of one row
     static_for<NB>([&](auto i) {
       static_for<NB>([&](auto j) {
         constexpr int I = decltype(i)::value, J = decltype(j)::value;
-        static_for<4>([&](auto r) {
-          constexpr int R = decltype(r)::value;
-          const int row = v2_row(I, R), col = v2_col(J);
-          stage[row * WT + (((col >> 2) ^ (row % ECPR)) << 2) + (col & 3)] = acc[I][J][R];
-        });
+        const int row = v2_row(I, 0), col = v2_col(J, 0);
+        *reinterpret_cast<floatx4*>(stage + row * WT + (((col >> 2) ^ (row % ECPR)) << 2)) =
+            acc[I][J];
       });
     });
   } else {

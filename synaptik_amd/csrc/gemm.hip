@@ -158,15 +158,17 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce4(GemmParams p, int spl
       const f4 mv = u.m != nullptr ? *reinterpret_cast<const f4*>(u.m + e) : f4{0.f, 0.f, 0.f, 0.f};
       const f4 vv = u.kind != 0 ? *reinterpret_cast<const f4*>(u.v + e) : f4{0.f, 0.f, 0.f, 0.f};
       f4 pc, mc, vc = f4{0.f, 0.f, 0.f, 0.f};
+      float chk = 0.0f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         float pe, me, ve = 0.0f;
-        if (u.kind == 0) ok &= sgd_element(u, uc.first, pv[c], v[c], mv[c], pe, me);
-        else ok &= adam_element(u, uc.k, pv[c], v[c], mv[c], vv[c], pe, me, ve);
+        if (u.kind == 0) sgd_element(u, uc.first, pv[c], v[c], mv[c], pe, me, chk);
+        else adam_element(u, uc.k, pv[c], v[c], mv[c], vv[c], pe, me, ve, chk);
         pc[c] = pe;
         mc[c] = me;
         vc[c] = ve;
       }
+      ok = ok && chk == 0.0f;
       *reinterpret_cast<f4*>(u.pn + e) = pc;
       if (u.mn != nullptr) *reinterpret_cast<f4*>(u.mn + e) = mc;
       if (u.kind != 0) *reinterpret_cast<f4*>(u.vn + e) = vc;

@@ -89,10 +89,10 @@ __device__ __forceinline__ UpdateCtx update_ctx(const GemmUpdate& u) {
 }
 __device__ __forceinline__ bool update_element(const GemmUpdate& u, const UpdateCtx& c,
                                                float pv, float g, float mv, float vv, int64_t e) {
-  float pc, mc, vc = 0.0f;
-  bool ok;
-  if (u.kind == 0) ok = sgd_element(u, c.first, pv, g, mv, pc, mc);
-  else ok = adam_element(u, c.k, pv, g, mv, vv, pc, mc, vc);
+  float pc, mc, vc = 0.0f, chk = 0.0f;
+  if (u.kind == 0) sgd_element(u, c.first, pv, g, mv, pc, mc, chk);
+  else adam_element(u, c.k, pv, g, mv, vv, pc, mc, vc, chk);
+  const bool ok = chk == 0.0f;
   u.pn[e] = pc;
   if (u.mn != nullptr) u.mn[e] = mc;
   if (u.kind != 0) u.vn[e] = vc;

@@ -475,6 +475,7 @@ gemm_f32_v2(GemmParams p) {
     const GemmUpdate& u = p.upd;
     const UpdateCtx uc = update_ctx(u);
     bool ok = uc.k.ok;
+    float chk = 0.0f;  // NaN once any intermediate of this lane's elements was not finite
     auto update_rows = [&](auto kindc) {
       constexpr bool SGD = decltype(kindc)::value == 0;
       for (int t = tfirst; t < tfirst + TSTEPS; ++t) {
@@ -489,8 +490,8 @@ gemm_f32_v2(GemmParams p) {
         static_for<4>([&](auto c) {
           constexpr int C = decltype(c)::value;
           float pe, me, ve = 0.0f;
-          if constexpr (SGD) ok &= sgd_element(u, uc.first, pv[C], gv[C], mv[C], pe, me);
-          else ok &= adam_element(u, uc.k, pv[C], gv[C], mv[C], vv[C], pe, me, ve);
+          if constexpr (SGD) sgd_element(u, uc.first, pv[C], gv[C], mv[C], pe, me, chk);
+          else adam_element(u, uc.k, pv[C], gv[C], mv[C], vv[C], pe, me, ve, chk);
           pc[C] = pe;
           mc[C] = me;
           vc[C] = ve;
@@ -502,7 +503,7 @@ gemm_f32_v2(GemmParams p) {
     };
     if (u.kind == 0) update_rows(std::integral_constant<int, 0>{});
     else update_rows(std::integral_constant<int, 1>{});
-    update_flag(u, uc, ok);
+    update_flag(u, uc, ok && chk == 0.0f);
     return;
   }
   const bool has_bias = p.bias != nullptr;

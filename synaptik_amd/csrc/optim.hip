@@ -100,19 +100,16 @@ __global__ void __launch_bounds__(OPT_NT) optimizer_kernel(OptParams p) {
       if (p.kind != 0) vv[q] = T.v[i0 + q];
     }
   }
+  float chk = 0.0f;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     if (q >= cnt) break;
     const float m0 = T.m != nullptr ? mv[q] : 0.0f;
     vc[q] = 0.0f;
-    bool e;
-    if (p.kind == 0) {
-      e = sgd_element(p, first, pv[q], gv[q], m0, pc[q], mc[q]);
-    } else {
-      e = adam_element(p, k, pv[q], gv[q], m0, vv[q], pc[q], mc[q], vc[q]);
-    }
-    ok &= e;
+    if (p.kind == 0) sgd_element(p, first, pv[q], gv[q], m0, pc[q], mc[q], chk);
+    else adam_element(p, k, pv[q], gv[q], m0, vv[q], pc[q], mc[q], vc[q], chk);
   }
+  ok = ok && chk == 0.0f;
   if (p.phase != 0) {
     float* dp = p.phase == 1 ? T.p : T.pn;
     float* dm = p.phase == 1 ? T.m : T.mn;

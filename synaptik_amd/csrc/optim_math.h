@@ -29,15 +29,25 @@ __device__ __forceinline__ Coeffs adam_coeffs(const P& p, int64_t step) {
   return k;
 }
 
-// One SGD element. Returns false if any intermediate is not finite.
+// Finiteness checks without lane-mask arithmetic: chk = fmaf(x, 0, chk) turns NaN as soon as one
+// checked value is +-inf or NaN and otherwise stays +0, so one comparison after a whole block of
+// elements (chk == 0) says whether every intermediate was finite. A comparison per check would
+// give a lane mask combined by scalar instructions, each waiting for the vector compare before
+// it; this is one vector FMA per check.
+__device__ __forceinline__ void check_finite(float x, float& chk) { chk = fmaf(x, 0.0f, chk); }
+__device__ __forceinline__ void check_positive(float x, float& chk) {
+  chk = x > 0.0f ? chk : __int_as_float(0x7fc00000);
+}
+
+// One SGD element; non-finite intermediates turn chk NaN.
 template <typename P>
-__device__ __forceinline__ bool sgd_element(const P& p, bool first, float pv, float g,
-                                            float mv, float& pc, float& mc) {
-  bool ok = is_finite(pv);
+__device__ __forceinline__ void sgd_element(const P& p, bool first, float pv, float g, float mv,
+                                            float& pc, float& mc, float& chk) {
+  check_finite(pv, chk);
   const float decay_term = p.weight_decay * pv;
-  ok &= is_finite(decay_term);
+  check_finite(decay_term, chk);
   const float adjusted = g + decay_term;
-  ok &= is_finite(adjusted);
+  check_finite(adjusted, chk);
   float selected = adjusted;
   mc = mv;
   if (p.momentum != 0.0f) {
@@ -46,18 +56,18 @@ __device__ __forceinline__ bool sgd_element(const P& p, bool first, float pv, fl
       um = adjusted;
     } else {
       const float mt = p.momentum * mv;
-      ok &= is_finite(mt);
+      check_finite(mt, chk);
       const float dg = (1.0f - p.dampening) * adjusted;
-      ok &= is_finite(dg);
+      check_finite(dg, chk);
       um = mt + dg;
     }
-    ok &= is_finite(um);
+    check_finite(um, chk);
     mc = um;
     if (p.nesterov) {
       const float look = p.momentum * um;
-      ok &= is_finite(look);
+      check_finite(look, chk);
       selected = adjusted + look;
-      ok &= is_finite(selected);
+      check_finite(selected, chk);
     } else {
       selected = um;
     }
@@ -65,60 +75,61 @@ __device__ __forceinline__ bool sgd_element(const P& p, bool first, float pv, fl
     mc = 0.0f;
   }
   const float scaled = p.lr * selected;
-  ok &= is_finite(scaled);
+  check_finite(scaled, chk);
   pc = pv - scaled;
-  ok &= is_finite(pc);
-  return ok;
+  check_finite(pc, chk);
 }
 
-// One Adam/AdamW element.
+// One Adam/AdamW element; non-finite intermediates and a denominator that is not positive turn
+// chk NaN.
 template <typename P>
-__device__ __forceinline__ bool adam_element(const P& p, const Coeffs& k, float pv,
-                                             float g0, float mv, float vv, float& pc, float& mc,
-                                             float& vc) {
-  bool ok = is_finite(pv);
+__device__ __forceinline__ void adam_element(const P& p, const Coeffs& k, float pv, float g0,
+                                             float mv, float vv, float& pc, float& mc, float& vc,
+                                             float& chk) {
+  check_finite(pv, chk);
   float gradient, base;
   if (p.kind == 2) {
     base = pv * k.decay_factor;
-    ok &= is_finite(base);
+    check_finite(base, chk);
     gradient = g0;
   } else {
     const float decay_term = p.weight_decay * pv;
-    ok &= is_finite(decay_term);
+    check_finite(decay_term, chk);
     gradient = g0 + decay_term;
-    ok &= is_finite(gradient);
+    check_finite(gradient, chk);
     base = pv;
   }
   const float first_term = p.beta1 * mv;
-  ok &= is_finite(first_term);
+  check_finite(first_term, chk);
   const float first_grad = (1.0f - p.beta1) * gradient;
-  ok &= is_finite(first_grad);
+  check_finite(first_grad, chk);
   const float first = first_term + first_grad;
-  ok &= is_finite(first);
+  check_finite(first, chk);
   const float squared = gradient * gradient;
-  ok &= is_finite(squared);
+  check_finite(squared, chk);
   const float second_term = p.beta2 * vv;
-  ok &= is_finite(second_term);
+  check_finite(second_term, chk);
   const float second_grad = (1.0f - p.beta2) * squared;
-  ok &= is_finite(second_grad);
+  check_finite(second_grad, chk);
   const float second = second_term + second_grad;
-  ok &= is_finite(second);
+  check_finite(second, chk);
   const float cf = first / k.c1;
   const float cs = second / k.c2;
-  ok &= is_finite(cf) && is_finite(cs);
+  check_finite(cf, chk);
+  check_finite(cs, chk);
   const float root = (float)sqrt((double)cs);
-  ok &= is_finite(root);
+  check_finite(root, chk);
   const float denom = root + p.eps;
-  ok &= is_finite(denom) && denom > 0.0f;
+  check_finite(denom, chk);
+  check_positive(denom, chk);
   const float numer = p.lr * cf;
-  ok &= is_finite(numer);
+  check_finite(numer, chk);
   const float update = numer / denom;
-  ok &= is_finite(update);
+  check_finite(update, chk);
   pc = base - update;
-  ok &= is_finite(pc);
+  check_finite(pc, chk);
   mc = first;
   vc = second;
-  return ok;
 }
 
 

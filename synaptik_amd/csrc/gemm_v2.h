@@ -466,6 +466,10 @@ gemm_f32_v2(GemmParams p) {
   };
   static_assert(KS == 1 || (WT / RSTEP) % KS == 0, "row steps split evenly between the groups");
   constexpr int TSTEPS = WT / RSTEP / KS;  // row steps per group
+  // row steps per chunk of the update loop (128-wide tiles: 16 row steps per lane; the 64-wide
+  // tiles' two measured faster unchunked)
+  constexpr int EPI_CH = BT == 128 ? 4 : 1;
+  static_assert(TSTEPS % EPI_CH == 0, "whole chunks");
   const int tfirst = kgroup * TSTEPS;
   const int64_t row_e = m0 + wm * WT + rg, col_e = n0 + wn * WT + 4 * q;
   const bool col_ok = !TAIL || col_e < p.N;  // N is a multiple of 4: whole segments
@@ -478,27 +482,40 @@ gemm_f32_v2(GemmParams p) {
     float chk = 0.0f;  // NaN once any intermediate of this lane's elements was not finite
     auto update_rows = [&](auto kindc) {
       constexpr bool SGD = decltype(kindc)::value == 0;
-      for (int t = tfirst; t < tfirst + TSTEPS; ++t) {
-        const int64_t row = row_e + RSTEP * t;
-        if (TAIL && (!col_ok || row >= p.M)) continue;
-        const int64_t e = row * p.N + col_e;
-        const floatx4 gv = tile_row(t);
-        const floatx4 pv = *reinterpret_cast<const floatx4*>(u.p + e);
-        const floatx4 mv = u.m != nullptr ? *reinterpret_cast<const floatx4*>(u.m + e) : floatx4{0.f, 0.f, 0.f, 0.f};
-        const floatx4 vv = SGD ? floatx4{0.f, 0.f, 0.f, 0.f} : *reinterpret_cast<const floatx4*>(u.v + e);
-        floatx4 pc, mc, vc = floatx4{0.f, 0.f, 0.f, 0.f};
-        static_for<4>([&](auto c) {
-          constexpr int C = decltype(c)::value;
-          float pe, me, ve = 0.0f;
-          if constexpr (SGD) sgd_element(u, uc.first, pv[C], gv[C], mv[C], pe, me, chk);
-          else adam_element(u, uc.k, pv[C], gv[C], mv[C], vv[C], pe, me, ve, chk);
-          pc[C] = pe;
-          mc[C] = me;
-          vc[C] = ve;
+      // EPI_CH row steps at a time: every parameter and slot load of the chunk is issued before
+      // its first store, so the loads' latencies overlap instead of adding up row after row
+      for (int t0 = tfirst; t0 < tfirst + TSTEPS; t0 += EPI_CH) {
+        floatx4 pv[EPI_CH], mv[EPI_CH], vv[EPI_CH];
+        static_for<EPI_CH>([&](auto ic) {
+          constexpr int I = decltype(ic)::value;
+          const int64_t row = row_e + RSTEP * (t0 + I);
+          const bool in = !TAIL || (col_ok && row < p.M);
+          const int64_t e = row * p.N + col_e;
+          const floatx4 z = floatx4{0.f, 0.f, 0.f, 0.f};
+          pv[I] = in ? *reinterpret_cast<const floatx4*>(u.p + e) : z;
+          mv[I] = in && u.m != nullptr ? *reinterpret_cast<const floatx4*>(u.m + e) : z;
+          vv[I] = !SGD && in ? *reinterpret_cast<const floatx4*>(u.v + e) : z;
         });
-        *reinterpret_cast<floatx4*>(u.pn + e) = pc;
-        if (u.mn != nullptr) *reinterpret_cast<floatx4*>(u.mn + e) = mc;
-        if constexpr (!SGD) *reinterpret_cast<floatx4*>(u.vn + e) = vc;
+        static_for<EPI_CH>([&](auto ic) {
+          constexpr int I = decltype(ic)::value;
+          const int64_t row = row_e + RSTEP * (t0 + I);
+          if (TAIL && (!col_ok || row >= p.M)) return;
+          const int64_t e = row * p.N + col_e;
+          const floatx4 gv = tile_row(t0 + I);
+          floatx4 pc, mc, vc = floatx4{0.f, 0.f, 0.f, 0.f};
+          static_for<4>([&](auto c) {
+            constexpr int C = decltype(c)::value;
+            float pe, me, ve = 0.0f;
+            if constexpr (SGD) sgd_element(u, uc.first, pv[I][C], gv[C], mv[I][C], pe, me, chk);
+            else adam_element(u, uc.k, pv[I][C], gv[C], mv[I][C], vv[I][C], pe, me, ve, chk);
+            pc[C] = pe;
+            mc[C] = me;
+            vc[C] = ve;
+          });
+          *reinterpret_cast<floatx4*>(u.pn + e) = pc;
+          if (u.mn != nullptr) *reinterpret_cast<floatx4*>(u.mn + e) = mc;
+          if constexpr (!SGD) *reinterpret_cast<floatx4*>(u.vn + e) = vc;
+        });
       }
     };
     if (u.kind == 0) update_rows(std::integral_constant<int, 0>{});

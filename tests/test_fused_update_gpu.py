@@ -25,9 +25,11 @@ OPTIMIZERS = [
 
 # (widths, batch): MFMA epilogue (odd extents, partial tiles); split-K reduction (few output
 # tiles, long batch); K == 1 (one row); the large-problem kernel (first layer's 2048x2048
-# weight gradient)
+# weight gradient, and a 2100x2000 one with ragged 128-wide tiles, whose update loads go a
+# chunk of row steps ahead with the rows past the edge masked)
 SHAPES = [([37, 130, 67, 3], 96), ([64, 96, 32, 1], 4096), ([16, 24, 8, 1], 1),
-          ([2048, 2048, 8], 64), ([784, 1024, 8], 1024), ([784, 1024, 10], 1024)]
+          ([2048, 2048, 8], 64), ([784, 1024, 8], 1024), ([784, 1024, 10], 1024),
+          ([2000, 2100, 8], 64)]
 
 
 def _run(ctx, monkeypatch, fuse, spec, Ws, bs, opt, x, y, steps):
@@ -43,7 +45,8 @@ def _bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
-@pytest.mark.parametrize("shape", SHAPES, ids=["tile", "splitk", "k1", "large", "edge64", "classifier"])
+@pytest.mark.parametrize("shape", SHAPES, ids=["tile", "splitk", "k1", "large", "edge64", "classifier",
+                                                 "large_ragged"])
 @pytest.mark.parametrize("opt", OPTIMIZERS, ids=["sgd", "nesterov", "dampening", "adam", "adamw"])
 def test_fused_update_matches_streaming_pass(ctx, monkeypatch, shape, opt):
     widths, batch = shape

@@ -7,9 +7,11 @@
 //   shift - (float)log(sum). The GPU forms the addends with exp_f32 (fexp.h), which returns
 //   that binary32 value or one of its neighbours (at most 1 ulp away; 0.8% of arguments), and
 //   rows held in registers multiply by a once-rounded reciprocal of the sum.
-//   The reference sums addends with Kahan compensation in binary32; the
-//   GPU sums the same binary32 addends in binary64 through a fixed tree and rounds once, so both
-//   sums are within a few binary32 ulps of the exact sum (reduction-order difference).
+//   The reference sums addends with Kahan compensation in binary32 (error within about
+//   2 ulp of the exact sum). Register-held rows sum each lane's 4V binary32 addends pairwise in
+//   binary32 (positive addends: error within log2(4V) ulp), combine the lanes in binary64
+//   through a fixed tree and round once; streamed rows sum in binary64 throughout. Both sums are
+//   within a few binary32 ulps of the exact sum (reduction-order difference).
 // One 256-thread workgroup owns one row; rows up to 4096 wide are held in registers
 // (one HBM read and one write per element), wider rows are streamed three times.
 #include "common.h"
@@ -137,7 +139,7 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restric
   // whole row takes the binary32 path of the exponential without a per-element range test.
   const bool in_range = shift == m && is_finite(m) && mn - m >= -87.0f;  // block-uniform
   float4 e[V];
-  double s = 0.0;
+  float part[V];
   if (in_range) {
 #pragma unroll
     for (int i = 0; i < V; ++i) {
@@ -147,7 +149,9 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restric
         e[i].y = exp_f32_in_range(v[i].y - shift);
         e[i].z = exp_f32_in_range(v[i].z - shift);
         e[i].w = exp_f32_in_range(v[i].w - shift);
-        s += ((double)e[i].x + (double)e[i].y) + ((double)e[i].z + (double)e[i].w);
+        part[i] = (e[i].x + e[i].y) + (e[i].z + e[i].w);
+      } else {
+        part[i] = 0.0f;
       }
     }
   } else {
@@ -159,11 +163,18 @@ __global__ void __launch_bounds__(SM_NT) softmax_fwd_regs(const float* __restric
         e[i].y = shifted_exp(v[i].y, shift);
         e[i].z = shifted_exp(v[i].z, shift);
         e[i].w = shifted_exp(v[i].w, shift);
-        s += ((double)e[i].x + (double)e[i].y) + ((double)e[i].z + (double)e[i].w);
+        part[i] = (e[i].x + e[i].y) + (e[i].z + e[i].w);
+      } else {
+        part[i] = 0.0f;
       }
     }
   }
-  const float sum = (float)block_sum<SM_NT>(s, dl);
+  // Pairwise over the lane's float4 groups (every part is >= 0 or NaN, so zero padding is exact).
+#pragma unroll
+  for (int h = 1; h < V; h <<= 1)
+#pragma unroll
+    for (int i = 0; i + h < V; i += 2 * h) part[i] += part[i + h];
+  const float sum = (float)block_sum<SM_NT>((double)part[0], dl);
   // Every lane needs the binary64 logarithm of the sum only for log-softmax; softmax needs it
   // only for the LSE output, which lane 0 forms below.
   const float logsum = log_softmax ? (float)log((double)sum) : 0.0f;

@@ -7,14 +7,17 @@
 // result is a normal float, and returns exactly the reference expression elsewhere.
 //
 // Method (Cody and Waite, "Software Manual for the Elementary Functions", 1980): write
-//   t = n ln2 + r,  n = rint(t / ln2),  |r| <= ln2 / 2,
-// with ln2 split into L1 = binary32(ln2) and L2 = binary32(ln2 - L1). Because L1 has 24
-// significant bits and |n| <= 127, t - n L1 is exactly representable and one FMA forms it
-// exactly; the second FMA subtracts n L2 with a single rounding. exp(r) = 1 + s with
-//   s = r + r^2 (1/2! + r (1/3! + ... + r / 7!)),
-// the Taylor series of exp - 1 truncated after degree 7 (truncation error below
-// 0.35^8 / 8! = 5.4e-9, i.e. below 0.1 ulp of 1), evaluated by Horner's rule with FMAs. The one
-// rounding of 1 + s dominates the error; scaling by 2^n with ldexp is exact in the normal range.
+//   t = n ln2 + r,  n = rint(t / ln2),  |r| <= ln2 / 2 (plus rounding),
+// with ln2 split into L1 = binary32(ln2) and L2 = binary32(ln2 - L1). n is formed by adding the
+// shifter 1.5 * 2^23 to t / ln2 in one FMA: the sum's spacing is 1, so the FMA rounds t / ln2 to
+// the nearest integer once, and the shifter's low mantissa bits then hold n (two's complement in
+// the bits that survive a shift left by 23). Because L1 has 24 significant bits and |n| <= 127,
+// t - n L1 is exactly representable and one FMA forms it exactly; the second FMA subtracts n L2
+// with a single rounding. exp(r) is the Taylor polynomial of degree 7 (truncation error below
+// 0.35^8 / 8! = 5.4e-9, i.e. below 0.1 ulp of 1) by Horner's rule with FMAs down to the constant
+// term, whose FMA rounds once; scaling by 2^n adds n to the exponent field, exact in the normal
+// range. Checked on the host against the binary64 expression for every 7th binary32 argument in
+// [-87, 88]: at most 1 ulp, 0.46% of arguments differ.
 //
 // Range: for t in [-87, 88] the result is a normal binary32 (n in [-126, 127], and for
 // n = -126 the reduced argument is positive). Outside it (overflow to +inf, subnormal results,
@@ -26,6 +29,7 @@
 // __device__ as nothing.
 #pragma once
 #include <math.h>
+#include <stdint.h>
 
 namespace shk {
 
@@ -34,8 +38,10 @@ __host__ __device__ inline float exp_f32_in_range(float t) {
   const float kLog2e = 0x1.715476p+0f;     // binary32(1 / ln 2)
   const float kLn2Hi = 0x1.62e430p-1f;     // L1 = binary32(ln 2)
   const float kLn2Lo = -0x1.05c610p-29f;   // L2 = binary32(ln 2 - L1)
-  const float n = rintf(t * kLog2e);
-  float r = fmaf(-n, kLn2Hi, t);  // exact
+  const float kShift = 0x1.8p23f;          // 1.5 * 2^23
+  const float k = fmaf(t, kLog2e, kShift);
+  const float n = k - kShift;              // exact
+  float r = fmaf(-n, kLn2Hi, t);           // exact
   r = fmaf(-n, kLn2Lo, r);
   float q = 0x1.a01a02p-13f;            // 1/7!
   q = fmaf(q, r, 0x1.6c16c2p-10f);      // 1/6!
@@ -43,8 +49,15 @@ __host__ __device__ inline float exp_f32_in_range(float t) {
   q = fmaf(q, r, 0x1.555556p-5f);       // 1/4!
   q = fmaf(q, r, 0x1.555556p-3f);       // 1/3!
   q = fmaf(q, r, 0.5f);                 // 1/2!
-  const float s = fmaf(r * r, q, r);
-  return ldexpf(1.0f + s, (int)n);
+  q = fmaf(q, r, 1.0f);                 // 1/1!
+  const float e = fmaf(q, r, 1.0f);     // 1/0!
+  uint32_t eb, kb;
+  __builtin_memcpy(&eb, &e, 4);
+  __builtin_memcpy(&kb, &k, 4);
+  eb += kb << 23;                       // n << 23 (mod 2^32): the low bits of k hold n
+  float out;
+  __builtin_memcpy(&out, &eb, 4);
+  return out;
 }
 
 __host__ __device__ inline float exp_f32(float t) {

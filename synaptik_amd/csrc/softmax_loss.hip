@@ -5,7 +5,7 @@
 //   -inf (log-softmax); a row containing -inf (and no NaN) is evaluated unshifted (shift 0);
 //   addends are (float)exp((double)(x - shift)); the result is (float)exp(shift)/sum or
 //   shift - (float)log(sum). The GPU forms the addends with exp_f32 (fexp.h), which returns
-//   that binary32 value or one of its neighbours (at most 1 ulp away; 0.8% of arguments), and
+//   that binary32 value or one of its neighbours (at most 1 ulp away; 0.46% of arguments), and
 //   rows held in registers multiply by a once-rounded reciprocal of the sum.
 //   The reference sums addends with Kahan compensation in binary32 (error within about
 //   2 ulp of the exact sum). Register-held rows sum each lane's 4V binary32 addends pairwise in

@@ -214,10 +214,11 @@ gemm_f32_v2(GemmParams p) {
   int64_t k_begin = p.kchunk > 0 ? (int64_t)blockIdx.y * p.kchunk : 0;
   int64_t k_len = p.kchunk > 0 ? std::min<int64_t>(p.kchunk, p.K - k_begin) : p.K;
   int nk = (int)((k_len + V2_BK - 1) / V2_BK);
-  if constexpr (KS == 2) {  // (no split-K slices with KS = 2)
+  if constexpr (KS == 2) {  // the two groups halve the slice [k_begin, k_begin + k_len)
     const int half = (nk + 1) / 2;
-    k_begin = (int64_t)kgroup * half * V2_BK;
-    k_len = kgroup == 0 ? std::min<int64_t>(p.K, (int64_t)half * V2_BK) : p.K - k_begin;
+    const int64_t len = k_len;
+    k_begin += (int64_t)kgroup * half * V2_BK;
+    k_len = kgroup == 0 ? std::min<int64_t>(len, (int64_t)half * V2_BK) : len - (int64_t)half * V2_BK;
     nk = half;  // group 1: k_len may end inside (or before) its last tile, which TAIL zero-fills
   }
   const float* a_tile = KA ? p.A + m0 * p.lda + k_begin : p.A + m0 + k_begin * p.lda;
@@ -396,7 +397,7 @@ gemm_f32_v2(GemmParams p) {
   // (row-major, 16-byte chunks XOR-swizzled by row) so that every global access of the epilogue
   // is a 16-byte row segment: lane (q = lane % ECPR, rg = lane / ECPR) owns columns 4q..4q+3 of
   // rows rg + (64 / ECPR) t, and each store instruction covers whole WT-float row segments.
-  if (p.partial != nullptr) {
+  if (KS == 1 && p.partial != nullptr) {
     // split-K: raw partial sums, reduced (and given the epilogue) by gemm_splitk_reduce
     float* part = p.partial + (int64_t)blockIdx.y * p.M * p.N;
     static_for<NB>([&](auto i) {
@@ -473,6 +474,19 @@ gemm_f32_v2(GemmParams p) {
   const int tfirst = kgroup * TSTEPS;
   const int64_t row_e = m0 + wm * WT + rg, col_e = n0 + wn * WT + 4 * q;
   const bool col_ok = !TAIL || col_e < p.N;  // N is a multiple of 4: whole segments
+  if constexpr (KS == 2) {
+    if (p.partial != nullptr) {
+      // split-K slice of a KS = 2 workgroup: the slice's partial sums (group 0's + group 1's),
+      // in 16-byte row segments, reduced (and given the epilogue) by gemm_splitk_reduce
+      float* part = p.partial + (int64_t)blockIdx.y * p.M * p.N;
+      for (int t = tfirst; t < tfirst + TSTEPS; ++t) {
+        const int64_t row = row_e + RSTEP * t;
+        if (TAIL && (!col_ok || row >= p.M)) continue;
+        *reinterpret_cast<floatx4*>(part + row * p.N + col_e) = tile_row(t);
+      }
+      return;
+    }
+  }
   // The loops below are compiled once per optimizer kind / (mode, activation, accumulate): a
   // runtime switch inside them would make every LDS read and store wait for the one before.
   if (p.upd.pn != nullptr) {
@@ -651,6 +665,14 @@ inline bool v2_split_in_group(const GemmParams& p, int bt) {
   return v2_ks2_enabled() && bt == 64 && p.kchunk == 0 && t64 < 512 && p.K >= 16 * V2_BK;
 }
 
+// In-workgroup split-K (KS = 2) for the split-K slices of 128x128 tiles: at most one workgroup
+// per CU (fewer than 512 tile slices) and at least eight k-tiles per group. Eight waves give each
+// SIMD two, as two four-wave workgroups per CU would, without more slices in HBM.
+inline bool v2_split_slices_in_group(const GemmParams& p, unsigned tiles, unsigned slices) {
+  return v2_ks2_enabled() && p.kchunk > 0 && p.partial != nullptr &&
+         (int64_t)tiles * slices < 512 && p.kchunk >= 16 * V2_BK;
+}
+
 template <bool TA, bool TB, int BT>
 hipError_t launch_v2_bt(const GemmParams& p, hipStream_t s) {
   g_colsum_rows = ((p.M + BT - 1) / BT) * 2;
@@ -672,6 +694,21 @@ hipError_t launch_v2_bt(const GemmParams& p, hipStream_t s) {
     }
   }
   const bool tail = p.M % BT != 0 || p.N % BT != 0 || span % V2_BK != 0 || p.K % V2_BK != 0;
+  if constexpr (BT == 128) {
+    if (v2_split_slices_in_group(p, tiles, slices)) {
+      // both groups whole k-tiles of every slice only when every slice, the last included, is a
+      // multiple of 2 BK
+      const bool tail2 = tail || span % (2 * V2_BK) != 0 ||
+                         (p.K - (int64_t)(slices - 1) * span) % (2 * V2_BK) != 0;
+      if (tail2)
+        hipLaunchKernelGGL((gemm_f32_v2<!TA, TB, BT, true, 2>), dim3(tiles, slices),
+                           dim3(2 * V2_NT), 0, s, p);
+      else
+        hipLaunchKernelGGL((gemm_f32_v2<!TA, TB, BT, false, 2>), dim3(tiles, slices),
+                           dim3(2 * V2_NT), 0, s, p);
+      return hipGetLastError();
+    }
+  }
   if (tail)
     hipLaunchKernelGGL((gemm_f32_v2<!TA, TB, BT, true, 1>), dim3(tiles, slices), dim3(V2_NT), 0, s, p);
   else

@@ -421,3 +421,42 @@ def test_split_in_group_gaussian_within_bound(ctx):
     gamma = K * u / (1 - K * u)
     bound = 2 * gamma * (np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64).T) + 1e-30
     assert (np.abs(C.astype(np.float64) - ref) <= bound).all()
+
+
+# In-workgroup split-K on the split-K slices of 128x128 tiles (fewer than 512 tile slices, slices
+# of at least 512 of K): each slice's two K groups are summed in LDS (group 0 + group 1) before
+# the slice's partial is stored; ragged last slices zero-fill group 1's missing k-tiles.
+KS2_SLICE_SHAPES = [(1024, 1024, 8192), (512, 1024, 8192), (1000, 1028, 5000), (640, 1024, 4096),
+                    (1024, 1000, 3000)]
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("shape", KS2_SLICE_SHAPES, ids=str)
+def test_split_slices_in_group_integer_bit_exact(ctx, shape, ta, tb):
+    M, N, K = shape
+    rng = np.random.default_rng(M + 5 * N + 11 * K + ta + 2 * tb)
+    A = rng.integers(-3, 4, size=(K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.integers(-3, 4, size=(N, K) if tb else (K, N)).astype(np.float32)
+    print(f"ks2 slices M={M} N={N} K={K} ta={ta} tb={tb}", flush=True)
+    C = _gemm_case(ctx, A, B, M, N, K, ta, tb)
+    assert np.array_equal(C, oracle.matmul(A, B, trans_a=ta, trans_b=tb))
+
+
+def test_split_slices_in_group_gaussian_bias_relu(ctx):
+    M, N, K = 1000, 1028, 5000
+    rng = np.random.default_rng(47)
+    A = rng.standard_normal((K, M)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    print(f"ks2 slices gaussian M={M} N={N} K={K}", flush=True)
+    C = _gemm_case(ctx, A, B, M, N, K, True, False, bias=b, act="relu")
+    Z = oracle.matmul(A, B, trans_a=True).astype(np.float64)
+    u = 2.0 ** -24
+    gamma = K * u / (1 - K * u)
+    bound = 2 * gamma * (np.abs(A).astype(np.float64).T @ np.abs(B).astype(np.float64)) + 1e-30
+    pre = Z + b
+    # where the pre-activation is decided beyond the bound, the ReLU output follows it exactly
+    decided = np.abs(pre) > bound + 1e-6 * np.abs(pre)
+    want = np.maximum(pre, 0.0)
+    assert (np.abs(C.astype(np.float64) - want)[decided] <= (bound + 1e-6 * np.abs(pre))[decided]).all()

@@ -544,36 +544,56 @@ gemm_f32_v2(GemmParams p) {
   auto store_rows = [&](auto modec, auto actc, auto accc) {
     constexpr int MODE = decltype(modec)::value, ACT = decltype(actc)::value;
     constexpr bool ACC = decltype(accc)::value;
-    for (int t = tfirst; t < tfirst + TSTEPS; ++t) {
-      const int64_t row = row_e + RSTEP * t;
-      if (TAIL && (!col_ok || row >= p.M)) continue;
-      floatx4 v = tile_row(t);
-      if constexpr (MODE != 1) {
-        if (has_bias) v = floatx4{v[0] + bias[0], v[1] + bias[1], v[2] + bias[2], v[3] + bias[3]};
-        static_for<4>([&](auto c) { v[decltype(c)::value] = apply_act(ACT, v[decltype(c)::value]); });
-      } else {
-        const floatx4 y = *reinterpret_cast<const floatx4*>(p.aux + row * p.ldaux + col_e);
-        static_for<4>([&](auto c) {
-          constexpr int C = decltype(c)::value;
-          v[C] = act_grad(ACT, v[C], y[C]);
+    // Modes 1 and 2 read one aux row segment per row step (the activation output, or dY): the
+    // loads of a chunk of SCH row steps are issued before the chunk's first store, so their
+    // latencies overlap instead of adding up row step after row step (the accumulators are
+    // staged in LDS by now, which frees their registers; 16 row steps at once would spill).
+    constexpr int SCH = TSTEPS < 8 ? TSTEPS : 8;
+    static_assert(TSTEPS % SCH == 0, "whole chunks");
+    for (int t0 = tfirst; t0 < tfirst + TSTEPS; t0 += SCH) {
+      floatx4 ya[SCH];
+      if constexpr (MODE != 0) {
+        static_for<SCH>([&](auto ic) {
+          constexpr int I = decltype(ic)::value;
+          const int64_t row = row_e + RSTEP * (t0 + I);
+          ya[I] = (!TAIL || (col_ok && row < p.M))
+                      ? *reinterpret_cast<const floatx4*>(p.aux + row * p.ldaux + col_e)
+                      : floatx4{0.f, 0.f, 0.f, 0.f};
         });
-      }
-      floatx4* dst = reinterpret_cast<floatx4*>(p.C + row * p.ldc + col_e);
-      if constexpr (ACC) {
-        const floatx4 o = *dst;
-        v = floatx4{o[0] + v[0], o[1] + v[1], o[2] + v[2], o[3] + v[3]};
-      }
-      *dst = v;
-      if constexpr (MODE == 2) {
-        // the cotangent of the activation input from the stored activation and dY
-        const floatx4 gy = *reinterpret_cast<const floatx4*>(p.aux + row * p.ldaux + col_e);
-        static_for<4>([&](auto c) {
-          constexpr int C = decltype(c)::value;
-          v[C] = act_grad(ACT, gy[C], v[C]);
-        });
-        *reinterpret_cast<floatx4*>(p.dz + row * p.ldaux + col_e) = v;
-      }
-      static_for<4>([&](auto c) { cs[decltype(c)::value] += (double)v[decltype(c)::value]; });
+    }
+      static_for<SCH>([&](auto ic) {
+        constexpr int I = decltype(ic)::value;
+        const int t = t0 + I;
+        const int64_t row = row_e + RSTEP * t;
+        if (TAIL && (!col_ok || row >= p.M)) return;
+        floatx4 v = tile_row(t);
+        if constexpr (MODE != 1) {
+          if (has_bias) v = floatx4{v[0] + bias[0], v[1] + bias[1], v[2] + bias[2], v[3] + bias[3]};
+          static_for<4>([&](auto c) { v[decltype(c)::value] = apply_act(ACT, v[decltype(c)::value]); });
+        } else {
+          const floatx4 y = ya[I];
+          static_for<4>([&](auto c) {
+            constexpr int C = decltype(c)::value;
+            v[C] = act_grad(ACT, v[C], y[C]);
+          });
+        }
+        floatx4* dst = reinterpret_cast<floatx4*>(p.C + row * p.ldc + col_e);
+        if constexpr (ACC) {
+          const floatx4 o = *dst;
+          v = floatx4{o[0] + v[0], o[1] + v[1], o[2] + v[2], o[3] + v[3]};
+        }
+        *dst = v;
+        if constexpr (MODE == 2) {
+          // the cotangent of the activation input from the stored activation and dY
+          const floatx4 gy = ya[I];
+          static_for<4>([&](auto c) {
+            constexpr int C = decltype(c)::value;
+            v[C] = act_grad(ACT, gy[C], v[C]);
+          });
+          *reinterpret_cast<floatx4*>(p.dz + row * p.ldaux + col_e) = v;
+        }
+        static_for<4>([&](auto c) { cs[decltype(c)::value] += (double)v[decltype(c)::value]; });
+      });
     }
   };
   auto by_acc = [&](auto modec, auto actc) {

@@ -460,3 +460,23 @@ def test_split_slices_in_group_gaussian_bias_relu(ctx):
     decided = np.abs(pre) > bound + 1e-6 * np.abs(pre)
     want = np.maximum(pre, 0.0)
     assert (np.abs(C.astype(np.float64) - want)[decided] <= (bound + 1e-6 * np.abs(pre))[decided]).all()
+
+
+@pytest.mark.parametrize("shape", [(1024, 1024, 8192), (1000, 1028, 5000)], ids=str)
+def test_split_slices_in_group_gradient_column_sum(ctx, shape):
+    """Activation-gradient epilogue and bias-gradient column sum on split-K slices run by eight-wave
+    workgroups: applied by the slice reduction after the slices are added in order."""
+    M, N, K = shape
+    rng = np.random.default_rng(53)
+    dZ = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    W = rng.integers(-3, 4, size=(K, N)).astype(np.float32)
+    y = oracle.activation("relu", rng.standard_normal((M, N)).astype(np.float32))
+    pb = ProgramBuilder()
+    sa, sb, sy = pb.input(M * K), pb.input(K * N), pb.input(M * N)
+    sc, sd = pb.output(M * N), pb.output(N)
+    pb.gemm(sa, sb, sc, M, N, K, aux=sy, act="relu", act_grad=True, colsum=sd)
+    print(f"ks2 slices gradient M={M} N={N} K={K}", flush=True)
+    C, db = run_program(ctx, pb, [dZ, W, y], [sc, sd])
+    ref = oracle.activation_grad("relu", oracle.matmul(dZ, W), y)
+    assert np.array_equal(C.reshape(M, N), ref)
+    np.testing.assert_array_max_ulp(db, oracle.colsum(ref), maxulp=1)

@@ -179,10 +179,11 @@ __device__ __forceinline__ void v2_barrier() {
 // The tile kernel. KA: A(m, k) is contiguous along k (A stored [M,K]); KB: B(n, k) is contiguous
 // along k (B stored [N,K]). KS = 2 splits K inside the workgroup: eight waves in two groups of
 // four, group h runs the whole pipeline below on k-tiles [h T, (h + 1) T), T = ceil(k-tiles / 2),
-// with LDS stages of its own (group 1's last tile is all zeros when the count is odd: TAIL), and
-// group 1 hands its accumulators to group 0 through LDS, which adds them (group 0 + group 1, a
-// fixed order) before the epilogue. It gives each SIMD two waves on problems with too few tiles
-// for two workgroups per CU, without partials in HBM or a second launch.
+// of the workgroup's K range (all of K, or its split-K slice), with LDS stages of its own (group
+// 1's last tile is all zeros when the count is odd: TAIL); both groups stage their partial tiles
+// in LDS and share the epilogue, each value the sum group 0 + group 1 (a fixed order), stored as
+// the result or, for a slice, as the slice's partial. It gives each SIMD two waves on problems
+// with too few tiles for two workgroups per CU, without more partials in HBM or a second launch.
 template <bool KA, bool KB, int BT, bool TAIL, int KS>
 __global__ void __launch_bounds__(V2_NT * KS) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_f32_v2(GemmParams p) {
@@ -560,7 +561,7 @@ gemm_f32_v2(GemmParams p) {
                       ? *reinterpret_cast<const floatx4*>(p.aux + row * p.ldaux + col_e)
                       : floatx4{0.f, 0.f, 0.f, 0.f};
         });
-    }
+      }
       static_for<SCH>([&](auto ic) {
         constexpr int I = decltype(ic)::value;
         const int t = t0 + I;

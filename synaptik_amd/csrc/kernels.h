@@ -141,6 +141,9 @@ struct CeHeadParams {
 hipError_t launch_ce_head(const CeHeadParams& p, hipStream_t s);
 // loss[0] = MEAN of row_loss[0 .. R) (binary64 sum, one rounding, divided by R).
 hipError_t launch_ce_head_finish(const float* row_loss, int64_t R, float* loss, hipStream_t s);
+// launch_ce_head_finish followed by launch_status_publish, as one launch
+hipError_t launch_ce_finish_publish(const float* row_loss, int64_t R, float* loss, uint32_t* status,
+                                   uint32_t* host_word, int64_t* commit_counter, hipStream_t s);
 
 // Interpreted fused elementwise chain (see pointwise.hip for the instruction set).
 struct PwInstr {

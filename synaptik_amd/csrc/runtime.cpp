@@ -259,6 +259,9 @@ struct Program {
   uint32_t side_steps = 0;
   std::vector<uint8_t> stream_of, record_after;
   std::vector<std::vector<uint32_t>> wait_for;
+  // A classifier-loss MEAN step (OP_CE_HEAD finish) that no later step depends on: unprofiled
+  // runs perform it in the run's publication kernel instead of a launch of its own (-1: none).
+  int64_t folded_finish = -1;
   // ---- settings and the lease pool, guarded by `mutex` ----
   std::mutex mutex;
   std::condition_variable lease_freed;
@@ -915,6 +918,29 @@ bool large_gemm(const Step& st) {
   return macs >= (double)(1ll << 28);
 }
 
+// The last OP_CE_HEAD finish step whose accesses conflict with no later step's (nothing later
+// reads the loss it writes or writes what it reads), so it can move to the end of the run.
+// SHK_HIP_FOLD_FINISH=0 keeps it a launch of its own.
+void plan_fold(Program* pr) {
+  static const bool on = [] {
+    const char* e = std::getenv("SHK_HIP_FOLD_FINISH");
+    return !(e != nullptr && e[0] == '0');
+  }();
+  pr->folded_finish = -1;
+  const size_t n = pr->steps.size();
+  const size_t launched = n > 0 && pr->steps[n - 1].rec.opcode == OP_STEP_COMMIT ? n - 1 : n;
+  if (!on) return;
+  for (size_t j = launched; j-- > 0;) {
+    const StepRecord& r = pr->steps[j].rec;
+    if (r.opcode != OP_CE_HEAD || r.iarg[4] != 1) continue;
+    const Access aj = step_access(pr->steps[j]);
+    for (size_t k = j + 1; k < launched; ++k)
+      if (accesses_conflict(aj, step_access(pr->steps[k]))) return;
+    pr->folded_finish = (int64_t)j;
+    return;
+  }
+}
+
 void plan_streams(Program* pr) {
   const size_t n = pr->steps.size();
   pr->stream_of.assign(n, 0);
@@ -965,21 +991,32 @@ hipError_t enqueue_steps(const Program& pr, Lease& ls, const Bound& b, hipStream
   if (n > 0 && pr.steps[n - 1].rec.opcode == OP_STEP_COMMIT)
     commit = b.get<int64_t>(pr.steps[n - 1].rec.slot[0]);
   const size_t launched = commit != nullptr ? n - 1 : n;
+  // the loss MEAN folded into the publication (not in profiled runs: their per-step events
+  // bracket every step's own launch)
+  const int64_t fold = profile ? -1 : pr.folded_finish;
+  auto publish = [&]() -> hipError_t {
+    if (fold < 0) return shk::launch_status_publish(ls.status, ls.host_status, commit, s0);
+    const StepRecord& r = pr.steps[(size_t)fold].rec;
+    return shk::launch_ce_finish_publish(b.get<const float>(r.slot[0]), r.iarg[0],
+                                         b.get<float>(r.slot[1]), ls.status, ls.host_status,
+                                         commit, s0);
+  };
   if (!two_streams || profile) {
     for (size_t i = 0; i < n; ++i) {
       if (profile && (e = hipEventRecord(ls.events[i], s0)) != hipSuccess) return e;
-      if (i < launched &&
+      if (i < launched && (int64_t)i != fold &&
           (e = enqueue_step(pr.steps[i], b, s0, ls.scratch, ls.status)) != hipSuccess)
         return e;
     }
     if (profile && (e = hipEventRecord(ls.events[n], s0)) != hipSuccess) return e;
-    return shk::launch_status_publish(ls.status, ls.host_status, commit, s0);
+    return publish();
   }
   hipStream_t s1 = side != nullptr ? side : pr.ctx->side_stream;
   if ((e = hipEventRecord(ls.fork, s0)) != hipSuccess ||
       (e = hipStreamWaitEvent(s1, ls.fork, 0)) != hipSuccess)
     return e;
   for (size_t j = 0; j < launched; ++j) {
+    if ((int64_t)j == fold) continue;  // no later step waits for it (plan_fold)
     const bool side = pr.stream_of[j] != 0;
     hipStream_t st = side ? s1 : s0;
     for (uint32_t i : pr.wait_for[j])
@@ -991,7 +1028,7 @@ hipError_t enqueue_steps(const Program& pr, Lease& ls, const Bound& b, hipStream
   }
   if ((e = hipEventRecord(ls.join, s1)) != hipSuccess) return e;
   if ((e = hipStreamWaitEvent(s0, ls.join, 0)) != hipSuccess) return e;
-  return shk::launch_status_publish(ls.status, ls.host_status, commit, s0);
+  return publish();
 }
 
 void destroy_lease(Lease* ls) {
@@ -1731,6 +1768,7 @@ int32_t decode_image(const void* image, uint64_t image_bytes, Program* pr) {
   pr->scratch_off = off;
   off += ((scratch_doubles * 8 + 255) / 256) * 256;
   plan_streams(pr);
+  plan_fold(pr);
   pr->scratch_side_off = off;
   if (pr->side_steps > 0) off += ((scratch_doubles * 8 + 255) / 256) * 256;
   pr->internal_offset.assign(h.n_slots, 0);

@@ -88,3 +88,29 @@ def test_fused_head_rejects_out_of_range_targets_and_keeps_state(ctx):
             assert np.array_equal(u, v)
     sess.run(x, np.zeros(8, np.int64))  # a valid batch still runs
     sess.close()
+
+
+@pytest.mark.parametrize("concurrent", [True, False])
+def test_loss_mean_folded_into_publication_matches_its_own_launch(ctx, concurrent):
+    """Unprofiled runs perform the fused head's loss MEAN inside the run's publication kernel;
+    profiled runs launch it as a step of its own. Both give the same objective after every step
+    and the same parameters and slots, on the two-stream schedule and on one stream."""
+    spec = MlpSpec.chain([784, 1024, 1024, 10], hidden="relu", loss="ce")
+    rng = np.random.default_rng(61)
+    x = rng.uniform(0, 1, (1024, 784)).astype(np.float32)
+    y = rng.integers(0, 10, 1024).astype(np.int64)
+    a = _session(ctx, spec, Adam(1e-3, 0.9, 0.999, 1e-8), 1024, True)
+    b = _session(ctx, spec, Adam(1e-3, 0.9, 0.999, 1e-8), 1024, True)
+    for sess in (a, b):
+        for prog, _ in sess._programs.values():
+            prog.set_concurrent(concurrent)
+    for prog, _ in b._programs.values():
+        prog.set_profiling(True)
+    for step in range(4):
+        la = a.run(x, y).objective
+        lb = b.run(x, y).objective
+        print(f"fold step={step} concurrent={concurrent} {la} {lb}", flush=True)
+        assert np.float32(la).view(np.uint32) == np.float32(lb).view(np.uint32)
+    _assert_state_identical(a, b)
+    a.close()
+    b.close()

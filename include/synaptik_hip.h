@@ -192,11 +192,22 @@ int32_t shk_hip_program_wait(void* program);
  * graph and creates no event or buffer: it clears the array with a kernel, launches the steps
  * on the context stream (the one-stream order), waits, and maps the status word as
  * shk_hip_program_run does. Pending asynchronous runs of the program are completed first.
- * Calls through one context are serialized; calls through different contexts of one device
- * share the array and race -- callers must not overlap them. Results equal shk_hip_program_run's
- * on a fresh lease. */
+ * Calls that use one device's array are serialized by a per-device lock, whichever contexts
+ * they go through (a call waits for the one in progress); the array keeps the last call's
+ * contents and each call clears it first. Results equal shk_hip_program_run's on a fresh lease. */
 int32_t shk_hip_program_run_static(void* program, uint32_t input_count, void* const* inputs,
                                    uint32_t output_count, void* const* outputs);
+/* The two-stream step schedule shk_hip_program_create would give an image, without a context or a
+ * device (HIP addition, for schedule checks): per step its stream (0 = the context stream, 1 = the
+ * side stream) and the one earlier step of the other stream it waits for (-1: none), and the loss
+ * MEAN step performed by the run's publication kernel instead of a launch of its own (-1: none).
+ * Steps keep program order on each stream; every side step starts after the run's fork from the
+ * context stream and the publication follows the join of both. out_steps receives the step count
+ * even when `capacity` is too small (INVALID_ARGUMENT). SHK_HIP_CONCURRENT=0 gives the one-stream
+ * plan. */
+int32_t shk_hip_program_plan(const void* image, uint64_t image_bytes, uint32_t capacity,
+                             uint8_t* out_stream, int32_t* out_wait, int64_t* out_folded,
+                             uint32_t* out_steps);
 /* Two-stream step schedule (HIP addition; on by default unless SHK_HIP_CONCURRENT=0 when the
  * program is created): at creation each step's slot reads and writes give its dependencies, and a
  * step that does not depend on the step at the tail of the context stream runs beside it on a

@@ -62,6 +62,10 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_address[kMaxDevices] = {};
 hipError_t g_scratch_error[kMaxDevices] = {};
+// One run at a time per device uses that device's copy of `scratch`: held by
+// shk_hip_program_run_static from the arena clear until its stream has drained, whichever
+// context the run goes through.
+std::mutex g_static_run_mutex[kMaxDevices];
 
 // Resolves this device's copy of `scratch` (the device current; once per device).
 void resolve_static_scratch(int device) {
@@ -830,8 +834,10 @@ hipError_t enqueue_step(const Step& st, const Bound& b, hipStream_t stream, doub
   }
 }
 
-// Slots a step reads and writes (and whether it reads the status word, which the other steps
-// only OR bits into). Reduction scratch is not a slot: each stream has its own.
+// Slots a step reads and writes, and whether it reads the status word (the step commit, the
+// optimizer's apply phase and its accumulator commit / clear, which act only on a clear word) or
+// only ORs bits into it (atomics: two such steps commute). Reduction scratch is not a slot: each
+// stream has its own, and steps on one stream run in program order.
 struct Access {
   std::vector<int32_t> r, w;
   bool status_read = false, status_or = false;
@@ -878,7 +884,10 @@ Access step_access(const Step& st) {
         W(e[i].pn); W(e[i].mn); W(e[i].vn);
       }
       R(sl[0]);
-      x.status_or = true;
+      // the apply phase and the accumulator commit / clear act only when the status word is
+      // clear: they read it, so they follow every step that can flag it
+      if (a[1] == 1 || a[0] == 4 || a[0] == 5) x.status_read = true;
+      if (a[0] == 3 || (a[0] <= 2 && a[1] != 1)) x.status_or = true;
       break;
     }
     case OP_STEP_COMMIT: R(sl[0]); W(sl[0]); x.status_read = true; break;
@@ -937,8 +946,18 @@ void plan_fold(Program* pr) {
     for (size_t k = j + 1; k < launched; ++k)
       if (accesses_conflict(aj, step_access(pr->steps[k]))) return;
     pr->folded_finish = (int64_t)j;
-    return;
+    break;
   }
+  // The folded step is never launched, so no event may be recorded after it and no step may
+  // wait for it: a capture would then wait on an event that was never recorded in it. plan_streams
+  // gives it no such edge when no later step conflicts with it (the same accesses_conflict);
+  // should the two ever disagree, the step stays a launch of its own.
+  const int64_t f = pr->folded_finish;
+  if (f < 0) return;
+  bool edge = f < (int64_t)pr->record_after.size() && pr->record_after[(size_t)f] != 0;
+  for (const auto& w : pr->wait_for)
+    for (uint32_t i : w) edge |= (int64_t)i == f;
+  if (edge) pr->folded_finish = -1;
 }
 
 void plan_streams(Program* pr) {
@@ -951,6 +970,8 @@ void plan_streams(Program* pr) {
   std::vector<Access> acc(n);
   for (size_t j = 0; j < n; ++j) acc[j] = step_access(pr->steps[j]);
   int64_t tail0 = -1;
+  // per stream: the latest step of the other stream its tail already follows (through a wait)
+  int64_t covered[2] = {-1, -1};
   for (size_t j = 0; j < n; ++j) {
     std::vector<uint32_t> deps;
     for (size_t i = 0; i < j; ++i)
@@ -965,11 +986,12 @@ void plan_streams(Program* pr) {
     pr->stream_of[j] = sj;
     if (sj == 0) tail0 = (int64_t)j;
     // stream order covers same-stream dependencies and the other stream's earlier ones
-    // behind its latest: one wait at most
+    // behind its latest: one wait at most, none when an earlier wait on this stream covers it
     int64_t latest = -1;
     for (uint32_t i : deps)
       if (pr->stream_of[i] != sj) latest = std::max<int64_t>(latest, i);
-    if (latest >= 0) {
+    if (latest > covered[sj]) {
+      covered[sj] = latest;
       pr->wait_for[j].push_back((uint32_t)latest);
       pr->record_after[latest] = 1;
     }
@@ -1871,6 +1893,37 @@ int32_t shk_hip_program_validate(const void* image, uint64_t image_bytes,
   }
 }
 
+int32_t shk_hip_program_plan(const void* image, uint64_t image_bytes, uint32_t capacity,
+                             uint8_t* out_stream, int32_t* out_wait, int64_t* out_folded,
+                             uint32_t* out_steps) {
+  if (out_steps != nullptr) *out_steps = 0;
+  if (out_folded != nullptr) *out_folded = -1;
+  if (image == nullptr || out_steps == nullptr)
+    return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "image or out_steps is null");
+  try {
+    Program pr;  // decoded and discarded; no context, no device
+    const int32_t st = decode_image(image, image_bytes, &pr);
+    pr.magic = 0;
+    if (st != SHK_HIP_STATUS_OK) return st;
+    const size_t n = pr.steps.size();
+    *out_steps = (uint32_t)n;
+    if (out_folded != nullptr) *out_folded = pr.folded_finish;
+    if (capacity < n || out_stream == nullptr || out_wait == nullptr)
+      return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "plan of %zu steps needs that capacity", n);
+    for (size_t j = 0; j < n; ++j) {
+      out_stream[j] = pr.stream_of[j];
+      if (pr.wait_for[j].size() > 1)
+        return fail(SHK_HIP_STATUS_INTERNAL_ERROR, "step %zu waits for more than one event", j);
+      out_wait[j] = pr.wait_for[j].empty() ? -1 : (int32_t)pr.wait_for[j][0];
+    }
+    return SHK_HIP_STATUS_OK;
+  } catch (const std::bad_alloc&) {
+    return fail(SHK_HIP_STATUS_ALLOCATION_FAILED, "host allocation failed");
+  } catch (...) {
+    return fail(SHK_HIP_STATUS_INTERNAL_ERROR, "unexpected exception");
+  }
+}
+
 int32_t shk_hip_program_release(void* program) {
   Program* pr = checked<Program, kProgramMagic>(program);
   if (pr == nullptr) return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "not a program handle");
@@ -2193,9 +2246,10 @@ int32_t run_program(void* program, uint32_t input_count, void* const* inputs, ui
 // The no-allocation run: the arena of the run (status word, reduction scratch, internal slots)
 // is this device's copy of `scratch`, cleared by a fill kernel first; the steps run on the
 // context stream alone, launched directly (no graph is captured or instantiated, no event is
-// created), and the run's status is published to the context's pinned word. The context mutex
-// is held from the first launch until the stream has drained, so runs through one context never
-// overlap; runs through two contexts of one device share the array and race.
+// created), and the run's status is published to the context's pinned word. The device's static
+// run mutex and then the context mutex are held from the arena clear until the stream has
+// drained, so two runs that share one device's array never overlap, whichever contexts they go
+// through.
 int32_t run_static(void* program, uint32_t input_count, void* const* inputs,
                    uint32_t output_count, void* const* outputs) {
   Program* pr = checked<Program, kProgramMagic>(program);
@@ -2234,6 +2288,8 @@ int32_t run_static(void* program, uint32_t input_count, void* const* inputs,
     view.scratch = reinterpret_cast<double*>(arena + pr->scratch_off);
     view.host_status = pr->ctx->host_status;
 
+    // device lock first, then the context's: no path takes them in the other order
+    std::lock_guard<std::mutex> device_lock(g_static_run_mutex[device]);
     std::lock_guard<std::mutex> ctx_lock(pr->ctx->mutex);
     HIP_TRY(hipSetDevice(device));
     hipStream_t stream = pr->ctx->stream;

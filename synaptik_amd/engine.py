@@ -352,7 +352,9 @@ class RunState:
 
 class PreparedExecution:
     """A prepared graph: the assembled schedule, its executables (immutable, shared by every
-    run) and the compositions that own them. close() releases the prepared resources once."""
+    run) and the compositions that own them. close() releases the prepared resources once: runs
+    that start after it has begun are rejected, and it waits for the runs in flight to finish
+    before the executables are closed."""
 
     def __init__(self, composition: HipEngineBackendComposition, schedule: PreparedSchedule,
                  graph: Partition):
@@ -360,17 +362,33 @@ class PreparedExecution:
         self.schedule = schedule
         self.graph = graph
         self._lock = threading.Lock()
+        self._idle = threading.Condition(self._lock)
+        self._in_flight = 0
         self._closed = False
 
-    def _require_open(self):
-        if self._closed:
-            raise RuntimeError("prepared execution is closed")  # IllegalStateException
+    def _enter(self):
+        with self._lock:
+            if self._closed:
+                raise RuntimeError("prepared execution is closed")  # IllegalStateException
+            self._in_flight += 1
+
+    def _leave(self):
+        with self._lock:
+            self._in_flight -= 1
+            if self._in_flight == 0:
+                self._idle.notify_all()
 
     def run(self, inputs: dict, maximum_bytes: int = 1 << 40) -> dict:
         """One run: borrows every caller input, creates the published buffers, executes the
         bound invocation synchronously and returns each publication as canonical big-endian
         bytes (HostTensorValue.java:18). The per-run buffers are released before returning."""
-        self._require_open()
+        self._enter()
+        try:
+            return self._run(inputs, maximum_bytes)
+        finally:
+            self._leave()
+
+    def _run(self, inputs: dict, maximum_bytes: int) -> dict:
         exe: HipPreparedExecutable = self.schedule.executables[0]
         plan = self.schedule.memory_plan
         state = RunState()
@@ -409,6 +427,8 @@ class PreparedExecution:
             if self._closed:
                 return
             self._closed = True
+            while self._in_flight:
+                self._idle.wait()
         for exe in self.schedule.executables:
             exe.close()
 
@@ -420,6 +440,7 @@ class Engine:
         self._compositions = list(compositions)
         self._lock = threading.Lock()
         self._closed = False
+        self._prepared: list[PreparedExecution] = []  # closed before the compositions
 
     @staticmethod
     def builder() -> "EngineBuilder":
@@ -470,14 +491,29 @@ class Engine:
         except BaseException:
             exe.close()  # the finalizer's acquisitions roll back on failure
             raise
-        return PreparedExecution(comp, schedule, graph)
+        execution = PreparedExecution(comp, schedule, graph)
+        with self._lock:
+            if not self._closed:
+                self._prepared.append(execution)
+                return execution
+        execution.close()  # the engine closed while this graph was being prepared
+        raise RuntimeError("engine is closed")
 
     def close(self) -> None:
+        """Closes every prepared execution (waiting for its runs in flight), then every
+        composition; each is closed even when an earlier one fails, and the first failure is
+        raised."""
         with self._lock:
             if self._closed:
                 return
             self._closed = True
+            prepared, self._prepared = self._prepared, []
         errors = []
+        for execution in prepared:
+            try:
+                execution.close()
+            except Exception as e:  # noqa: BLE001
+                errors.append(e)
         for comp in self._compositions:
             try:
                 comp.close()

@@ -69,6 +69,7 @@ EXPORTED_SYMBOLS = (
     "shk_hip_program_lease_count",
     "shk_hip_program_run_static",
     "shk_hip_program_validate",
+    "shk_hip_program_plan",
     "shk_hip_program_set_profiling",
     "shk_hip_program_step_times",
     "shk_hip_program_step_count",
@@ -160,6 +161,9 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
             "shk_hip_program_arena_bytes": (i32, [vp, ctypes.POINTER(u64)]),
             "shk_hip_program_lease_count": (i32, [vp, ctypes.POINTER(u32)]),
             "shk_hip_program_validate": (i32, [vp, u64, ctypes.POINTER(u64)]),
+            "shk_hip_program_plan": (i32, [vp, u64, u32, ctypes.POINTER(ctypes.c_uint8),
+                                           ctypes.POINTER(ctypes.c_int32),
+                                           ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(u32)]),
             "shk_hip_program_run_static": (i32, [vp, u32, ctypes.POINTER(vp), u32,
                                                  ctypes.POINTER(vp)]),
             "shk_hip_program_set_profiling": (i32, [vp, i32]),
@@ -259,6 +263,26 @@ def validate_program_image(image: bytes) -> int:
     buf = ctypes.create_string_buffer(bytes(image), max(1, len(image)))
     check(lib, lib.shk_hip_program_validate(buf, len(image), ctypes.byref(out)))
     return out.value
+
+
+def program_plan(image: bytes):
+    """The two-stream schedule program creation gives an image, without a device
+    (`shk_hip_program_plan`): (stream per step, the step each waits for or -1, the loss MEAN step
+    folded into the publication or -1)."""
+    lib = load_library()
+    buf = ctypes.create_string_buffer(bytes(image), max(1, len(image)))
+    n = ctypes.c_uint32()
+    folded = ctypes.c_int64()
+    st = lib.shk_hip_program_plan(buf, len(image), 0, None, None, ctypes.byref(folded),
+                                  ctypes.byref(n))
+    if n.value == 0:
+        check(lib, st)
+        return [], [], -1
+    streams = (ctypes.c_uint8 * n.value)()
+    waits = (ctypes.c_int32 * n.value)()
+    check(lib, lib.shk_hip_program_plan(buf, len(image), n.value, streams, waits,
+                                        ctypes.byref(folded), ctypes.byref(n)))
+    return list(streams), list(waits), folded.value
 
 
 def storage_transfer_bytes(element_width: int, shape, strides, storage_offset: int) -> int:

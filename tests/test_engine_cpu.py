@@ -132,3 +132,64 @@ def test_schedule_needs_a_preparation_per_buffer_and_a_creator_per_workspace():
         PreparedSchedule(plan, ((CallerInput(),), (CallerInput(),)), (), (), (), ())
     with pytest.raises(ValueError, match="must not be empty"):
         PreparedSchedule(plan, ((CallerInput(),), ()), (None,), (), (), ())
+
+
+class _FakeExecutable:
+    def __init__(self, log):
+        self.log = log
+
+    def close(self):
+        self.log.append("executable closed")
+
+
+def _execution(log):
+    from synaptik_amd.engine import PreparedExecution
+
+    class Schedule:
+        executables = (_FakeExecutable(log),)
+
+    return PreparedExecution(FakeComposition(), Schedule(), None)
+
+
+def test_close_waits_for_runs_in_flight_and_rejects_new_ones():
+    """PreparedExecution.close during a run: the run finishes on open executables, close returns
+    only after it, and later runs are rejected (IllegalStateException)."""
+    import threading
+    log = []
+    pe = _execution(log)
+    started, release = threading.Event(), threading.Event()
+
+    def slow_run(inputs, maximum_bytes):
+        started.set()
+        release.wait(5)
+        log.append("run finished")
+        return {}
+
+    pe._run = slow_run
+    runner = threading.Thread(target=pe.run, args=({},))
+    runner.start()
+    assert started.wait(5)
+    closer = threading.Thread(target=pe.close)
+    closer.start()
+    closer.join(0.2)
+    assert closer.is_alive() and log == []  # waiting for the run
+    with pytest.raises(RuntimeError, match="closed"):
+        pe.run({})
+    release.set()
+    runner.join(5)
+    closer.join(5)
+    assert log == ["run finished", "executable closed"]
+    pe.close()  # idempotent
+    assert log == ["run finished", "executable closed"]
+
+
+def test_engine_close_closes_prepared_executions_before_compositions():
+    log = []
+    comp = FakeComposition()
+    comp.close = lambda: log.append("composition closed")
+    engine = Engine([comp])
+    engine._prepared.append(_execution(log))
+    engine.close()
+    assert log == ["executable closed", "composition closed"]
+    with pytest.raises(RuntimeError, match="closed"):
+        engine.prepare(None)

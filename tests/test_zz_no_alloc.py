@@ -109,3 +109,43 @@ def test_programs_beyond_the_static_array_are_refused(ctx):
     with pytest.raises(HipInvalidArgument, match="at most"):
         prog.run_static(ins, [ctx.buffer(8192 * 4096 * 4)])
     prog.close()
+
+
+def test_calls_through_two_contexts_of_one_device_do_not_interfere():
+    """Two contexts of device 0, each with a program of its own, call run_static from two threads
+    at once. The calls share the device's array; the per-device lock serializes them, so every
+    result equals that context's leased run bit for bit."""
+    import threading
+
+    from synaptik_amd.native import HipContext
+
+    rng = np.random.default_rng(4)
+    jobs = []
+    for R, C in ((2048, 333), (1500, 64)):
+        c = HipContext(0)
+        pb, outs = _loss_program(R, C)
+        prog = HipProgram(c, pb.image())
+        x = c.upload((rng.standard_normal((R, C)) * 3).astype(np.float32))
+        lab = c.upload(rng.integers(0, C, R).astype(np.int64))
+        w = [c.buffer(s.nbytes) for s in outs]
+        prog.run([x, lab], w)
+        want = [b.download(np.float32, s.count) for b, s in zip(w, outs)]
+        jobs.append(dict(ctx=c, prog=prog, ins=[x, lab], outs=outs, want=want, bad=[]))
+
+    def work(j):
+        o = [j["ctx"].buffer(s.nbytes) for s in j["outs"]]
+        for it in range(25):
+            j["prog"].run_static(j["ins"], o)
+            for k, (b, s) in enumerate(zip(o, j["outs"])):
+                if not np.array_equal(_bits(b.download(np.float32, s.count)), _bits(j["want"][k])):
+                    j["bad"].append((it, k))
+
+    threads = [threading.Thread(target=work, args=(j,)) for j in jobs]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    for j in jobs:
+        assert not j["bad"], j["bad"][:5]
+        j["prog"].close()
+        j["ctx"].close()

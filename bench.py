@@ -55,7 +55,7 @@ def measured_gemm_traffic():
 def build_session(ctx, seed=0):
     from synaptik_amd.training import HipTrainingSession, MlpSpec, Sgd, init_parameters
     spec = MlpSpec.chain([WIDTH] * (LAYERS + 1), hidden="relu", loss="mse")
-    Ws, bs = init_parameters(spec, seed, "he_normal")
+    Ws, bs = init_parameters(spec, seed, "builder_he_normal")
     sess = HipTrainingSession.open(ctx, spec, Ws, bs, Sgd(LR, momentum=MOMENTUM), BATCH)
     rng = np.random.default_rng(seed + 1)
     x = ctx.upload(rng.standard_normal((BATCH, WIDTH), dtype=np.float32))
@@ -68,7 +68,7 @@ def cpu_baseline(sample_batch: int, seed=0) -> dict:
     from oracle import oracle
     from synaptik_amd.training import MlpSpec, init_parameters
     spec = MlpSpec.chain([WIDTH] * (LAYERS + 1), hidden="relu", loss="mse")
-    Ws, bs = init_parameters(spec, seed, "he_normal")
+    Ws, bs = init_parameters(spec, seed, "builder_he_normal")
     model = oracle.OracleMLP(Ws, bs, ["relu"] * (LAYERS - 1) + [None], "mse",
                              dict(kind="sgd", lr=LR, momentum=MOMENTUM))
     rng = np.random.default_rng(seed + 1)
@@ -177,7 +177,7 @@ def c3_line(ctx, rng, one_stream: bool = False) -> dict:
     whose per-kernel times are not shared with concurrent work)."""
     from synaptik_amd.training import Adam, HipTrainingSession, MlpSpec, init_parameters
     spec = MlpSpec.chain([784, 1024, 1024, 10], hidden="relu", loss="ce")
-    Ws, bs = init_parameters(spec, 0, "he_normal")
+    Ws, bs = init_parameters(spec, 0, "builder_he_normal")
     sess = HipTrainingSession.open(ctx, spec, Ws, bs, Adam(1e-3, 0.9, 0.999, 1e-8), 1024)
     if one_stream:
         sess.program.set_concurrent(False)
@@ -304,7 +304,12 @@ def secondary(ctx, reps: int = 5, cpu: bool = True) -> dict:
     B, I, O = 8192, 1024, 1024
     pb, outs = lower_dense_layer(B, I, O, "relu", "in_out")
     prog = HipProgram(ctx, pb.image())
-    ins = [ctx.upload(rng.standard_normal(n, dtype=np.float32)) for n in (B * I, I * O, O, B * O)]
+    # X, dY ~ N(0,1); W Xavier-uniform (bound sqrt(6 / (in + out))); b zeros
+    xb = float(np.sqrt(6.0 / (I + O)))
+    ins = [ctx.upload(rng.standard_normal(B * I, dtype=np.float32)),
+           ctx.upload(rng.uniform(-xb, xb, I * O).astype(np.float32)),
+           ctx.upload(np.zeros(O, np.float32)),
+           ctx.upload(rng.standard_normal(B * O, dtype=np.float32))]
     obs = [ctx.buffer(s.nbytes) for s in outs]
     for _ in range(5):
         prog.run(ins, obs)
@@ -449,7 +454,7 @@ def add_cpu_baselines(out: dict) -> None:
         "extrapolated": False, "sample": f"the full layer, {B} rows ({dt:.2f} s)"}
     # C3: one complete Adam step of the classifier on all 1024 rows
     spec = MlpSpec.chain([784, 1024, 1024, 10], hidden="relu", loss="ce")
-    Ws, bs = init_parameters(spec, 0, "he_normal")
+    Ws, bs = init_parameters(spec, 0, "builder_he_normal")
     model = oracle.OracleMLP(Ws, bs, ["relu", "relu", None], "ce",
                              dict(kind="adam", lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8))
     xb = rng.uniform(0, 1, (1024, 784)).astype(np.float32)

@@ -33,6 +33,20 @@ int32_t shk_lxm_uniform_f64(uint64_t* state, double origin, double bound, uint64
 int32_t shk_lxm_uniform_f32(uint64_t* state, double origin, double bound, uint64_t count,
                             float* out);
 
+/* count successive nextGaussian() values: McFarland's modified ziggurat (J. Stat. Comput. Simul.
+ * 86(7), 2016), the method of RandomSupport.computeNextGaussian that RandomGenerator.nextGaussian()
+ * uses, with tables built from that construction at first use (TensorRandoms.sampleFloat32 /
+ * sampleFloat64, TensorRandoms.java:615-656: one call per element). */
+int32_t shk_lxm_next_gaussian(uint64_t* state, uint64_t count, double* out);
+/* The ziggurat's tables, for checks: out_layers receives R (rectangles) and out_box_area the area
+ * A = sqrt(pi/2) / 256 of each of the 256 boxes; with capacity >= 257, out_x[0..R] receives
+ * x_0 > ... > x_{R-1} > x_R = 0, out_region_area[0..R] the areas of the tail, the overhangs and
+ * the cap, and out_threshold / out_alias the 256 columns of the alias table (thresholds over
+ * 2^56). */
+int32_t shk_lxm_gaussian_tables(uint32_t capacity, double* out_x, double* out_region_area,
+                                uint64_t* out_threshold, uint16_t* out_alias,
+                                uint32_t* out_layers, double* out_box_area);
+
 #ifdef __cplusplus
 }
 #endif

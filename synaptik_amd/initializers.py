@@ -11,9 +11,9 @@
   offer `uniform_block(origin, bound, count, dtype)` / `gaussian_block(count)` to draw many values
   in one call, with the same values as the per-element calls.
 * `L64X128MixRandom(seed)`: the generator ModelBuilder and Linear use (ModelBuilder.java:74-76),
-  restated natively in libsynaptik_hip.so (csrc/lxm.cpp). Its `next_gaussian` is not provided:
-  the JDK draws Gaussians with a table-driven modified ziggurat whose tables this build does not
-  restate, so Gaussian policies need another Gaussian source.
+  restated natively in libsynaptik_hip.so (csrc/lxm.cpp), with `next_gaussian` as McFarland's
+  modified ziggurat (the method of the JDK's RandomSupport.computeNextGaussian; tables built from
+  that construction, so whether they equal the JDK's bit for bit is not checked).
 * `builder_parameters(spec, seed)`: the weights and biases `Model.builder().seed(seed)` creates
   for a Linear chain: appended step i (Linear layers and activation steps both count) gets a
   fresh L64X128MixRandom(seed + 0x9E3779B97F4A7C15 * i) with long wraparound; weights are
@@ -48,8 +48,15 @@ def _native():
                                           ctypes.POINTER(ctypes.c_double)]
         L.shk_lxm_uniform_f32.argtypes = [u64p, ctypes.c_double, ctypes.c_double, ctypes.c_uint64,
                                           ctypes.POINTER(ctypes.c_float)]
+        L.shk_lxm_next_gaussian.argtypes = [u64p, ctypes.c_uint64, ctypes.POINTER(ctypes.c_double)]
+        L.shk_lxm_gaussian_tables.argtypes = [ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
+                                              ctypes.POINTER(ctypes.c_double), u64p,
+                                              ctypes.POINTER(ctypes.c_uint16),
+                                              ctypes.POINTER(ctypes.c_uint32),
+                                              ctypes.POINTER(ctypes.c_double)]
         for fn in (L.shk_lxm_seed, L.shk_lxm_next_long, L.shk_lxm_next_double,
-                   L.shk_lxm_uniform_f64, L.shk_lxm_uniform_f32):
+                   L.shk_lxm_uniform_f64, L.shk_lxm_uniform_f32, L.shk_lxm_next_gaussian,
+                   L.shk_lxm_gaussian_tables):
             fn.restype = ctypes.c_int32
         _lib = L
     return _lib
@@ -118,10 +125,37 @@ class L64X128MixRandom:
             return float(self.next_doubles(1)[0])
         return float(self.uniform_block(origin, bound, 1, np.float64)[0])
 
+    def gaussian_block(self, count: int) -> np.ndarray:
+        """count successive nextGaussian() draws (binary64)."""
+        out = np.empty(count, np.float64)
+        if _native().shk_lxm_next_gaussian(self._state, count,
+                                           out.ctypes.data_as(ctypes.POINTER(ctypes.c_double))):
+            raise RuntimeError("shk_lxm_next_gaussian failed")
+        return out
+
     def next_gaussian(self) -> float:
-        raise NotImplementedError(
-            "L64X128MixRandom.nextGaussian (the JDK's modified-ziggurat tables) is not restated; "
-            "supply a Gaussian source for normal initialization policies")
+        return float(self.gaussian_block(1)[0])
+
+
+def gaussian_tables() -> dict:
+    """The nextGaussian ziggurat's tables (shk_lxm_gaussian_tables): layers R, box area A, x[0..R],
+    region areas (tail, overhangs, cap), alias thresholds (over 2^56) and alias columns."""
+    L = _native()
+    x = np.zeros(257, np.float64)
+    area = np.zeros(257, np.float64)
+    thr = np.zeros(256, np.uint64)
+    alias = np.zeros(256, np.uint16)
+    layers = ctypes.c_uint32()
+    box = ctypes.c_double()
+    if L.shk_lxm_gaussian_tables(257, x.ctypes.data_as(ctypes.POINTER(ctypes.c_double)),
+                                 area.ctypes.data_as(ctypes.POINTER(ctypes.c_double)),
+                                 thr.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)),
+                                 alias.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)),
+                                 ctypes.byref(layers), ctypes.byref(box)):
+        raise RuntimeError("shk_lxm_gaussian_tables failed")
+    R = layers.value
+    return dict(layers=R, box_area=box.value, x=x[:R + 1].copy(), region_area=area[:R + 1].copy(),
+                threshold=thr, alias=alias)
 
 
 # ---- policies (ParameterInitialization) ----

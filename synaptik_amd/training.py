@@ -153,12 +153,17 @@ def init_parameters(spec: MlpSpec, seed: int, scheme: str):
 
     'builder': what `Model.builder().seed(seed)` creates for this Linear chain -- Glorot-uniform
     weights from one L64X128MixRandom per builder step (initializers.builder_parameters).
+    'builder_he_normal': the same generators and step seeds with Linear's kaimingReluNormal policy
+    (sigma sqrt(2 / fanIn), one nextGaussian per weight in row-major order).
     'xavier_uniform' (bound sqrt(6/(fan_in+fan_out))) and 'he_normal' (sigma sqrt(2/fan_in)) draw
     the same distributions as ParameterInitializers.java:269-372 from numpy's generator instead,
     for seeded synthetic inputs."""
     if scheme == "builder":
         from .initializers import builder_parameters
         return builder_parameters(spec, seed)
+    if scheme == "builder_he_normal":
+        from .initializers import ParameterInitialization, builder_parameters
+        return builder_parameters(spec, seed, policy=ParameterInitialization("kaiming_relu_normal"))
     rng = np.random.default_rng(seed)
     Ws, bs = [], []
     for l in spec.layers:

@@ -296,11 +296,157 @@ def test_doubles_grid_range_and_uniformity():
         I.L64X128MixRandom(3).uniform_block(-1e308, 1e308, 1, np.float64)
 
 
-def test_nearby_seeds_give_unrelated_streams_and_gaussian_is_refused():
+def test_nearby_seeds_give_unrelated_streams():
     a = I.L64X128MixRandom(0).next_doubles(50_000)
     b = I.L64X128MixRandom(1).next_doubles(50_000)
     assert abs(np.corrcoef(a, b)[0, 1]) < 0.02
-    with pytest.raises(NotImplementedError):
-        I.L64X128MixRandom(0).next_gaussian()
-    with pytest.raises(NotImplementedError):
-        I.glorot_normal((2, 2), "FLOAT32", I.L64X128MixRandom(0))
+    ga = I.L64X128MixRandom(0).gaussian_block(50_000)
+    gb = I.L64X128MixRandom(1).gaussian_block(50_000)
+    assert abs(np.corrcoef(ga, gb)[0, 1]) < 0.02
+
+
+# ---- nextGaussian: McFarland's modified ziggurat (tables from its construction) ----
+def _f(x):
+    return np.exp(-0.5 * np.asarray(x, np.float64) ** 2)
+
+
+def test_ziggurat_layers_have_equal_area_and_fill_the_half_normal():
+    """256 boxes of area A = sqrt(pi/2)/256: rectangle 0 is [0, x0] x [0, f(x0)], rectangle k is
+    [0, x_k] x [f(x_{k-1}), f(x_k)], each of area A, widths strictly decreasing; no further
+    rectangle of area A fits under the curve above the last; the tail, overhang and cap areas,
+    integrated independently, add up with the rectangles to the whole half-normal area."""
+    from scipy import integrate, special
+    t = I.gaussian_tables()
+    R, A, x = t["layers"], t["box_area"], t["x"]
+    T = math.sqrt(math.pi / 2)
+    assert A == pytest.approx(T / 256, rel=1e-15)
+    assert R == 253 and x[R] == 0.0 and len(x) == R + 1
+    assert np.all(np.diff(x) < 0)
+    assert x[0] * _f(x[0]) == pytest.approx(A, rel=1e-13)
+    assert x[0] > 1.0  # the larger root of x f(x) = A
+    for k in range(1, R):
+        assert x[k] * (_f(x[k]) - _f(x[k - 1])) == pytest.approx(A, rel=1e-9), k
+    xs = np.linspace(0, x[R - 1], 200_001)
+    assert np.max(xs * (_f(xs) - _f(x[R - 1]))) < A  # the cap holds no further rectangle
+    area = t["region_area"]
+    assert area[0] == pytest.approx(T * special.erfc(x[0] / math.sqrt(2)), rel=1e-9)
+    for k in range(1, R):
+        want = integrate.quad(lambda u: math.exp(-0.5 * u * u) - _f(x[k - 1]), x[k], x[k - 1],
+                              epsabs=0, epsrel=1e-12)[0]
+        assert area[k] == pytest.approx(want, rel=1e-7, abs=1e-16), k
+    cap = integrate.quad(lambda u: math.exp(-0.5 * u * u) - _f(x[R - 1]), 0, x[R - 1],
+                         epsabs=0, epsrel=1e-12)[0]
+    assert area[R] == pytest.approx(cap, rel=1e-9)
+    assert np.all(area > 0)
+    assert R * A + area.sum() == pytest.approx(T, rel=1e-12)
+    assert area.sum() == pytest.approx((256 - R) * A, rel=1e-9)
+
+
+def test_ziggurat_alias_table_reproduces_the_region_probabilities():
+    """Walker's alias table over 256 columns: each region's probability (column j kept with
+    threshold_j / 2^56, else sent to alias_j) equals its area over the slow path's total."""
+    t = I.gaussian_tables()
+    R, thr, alias, area = t["layers"], t["threshold"], t["alias"], t["region_area"]
+    keep = thr.astype(np.float64) / 2.0**56
+    assert np.all((keep >= 0) & (keep <= 1)) and np.all(alias <= R)
+    prob = np.zeros(R + 1)
+    for j in range(256):
+        if j <= R:
+            prob[j] += keep[j] / 256
+        else:
+            assert keep[j] == 0.0  # unused columns always take their alias
+        prob[alias[j]] += (1 - keep[j]) / 256
+    np.testing.assert_allclose(prob, area / area.sum(), rtol=0, atol=2.0**-52)
+
+
+def test_gaussian_fast_path_is_the_rectangle_closed_form():
+    """A draw whose first nextLong picks a rectangle (low 8 bits < R) is x_box * U1 * 2^-63 of that
+    one long and consumes nothing else; the slow path consumes at least two longs. Checked by
+    following the long stream of an identically seeded generator."""
+    t = I.gaussian_tables()
+    R, x = t["layers"], t["x"]
+    gen = I.L64X128MixRandom(1234)
+    fast = slow = 0
+    for _ in range(3000):
+        c = I.L64X128MixRandom(0)
+        c._state[:] = gen._state[:]
+        v = gen.next_gaussian()
+        u1 = c.next_long()
+        box = u1 & 0xFF
+        if box < R:
+            assert v == math.ldexp(x[box], -63) * float(u1)
+            assert gen.state == c.state  # exactly one long
+            fast += 1
+        else:
+            assert math.copysign(1.0, v) == (-1.0 if u1 < 0 else 1.0)  # the sign is U1's
+            assert gen.state != c.state  # more than the one long
+            slow += 1
+    assert fast + slow == 3000 and slow > 0
+    assert fast / 3000 == pytest.approx(R / 256, abs=0.02)
+
+
+def test_gaussian_draws_follow_the_standard_normal():
+    """4M draws: moments, Kolmogorov-Smirnov against Phi, a chi-square over the ziggurat's own
+    layer boundaries (which would see a wrong overhang or cap), the tail beyond x0 (its mass and,
+    conditionally, its shape), and sign symmetry."""
+    from scipy import special, stats
+    t = I.gaussian_tables()
+    x = t["x"]
+    d = I.L64X128MixRandom(20240607).gaussian_block(4_000_000)
+    n = d.size
+    assert abs(d.mean()) < 5 / math.sqrt(n)
+    assert d.var() == pytest.approx(1.0, abs=5 * math.sqrt(2 / n))
+    assert abs(stats.skew(d)) < 5 * math.sqrt(6 / n)
+    assert abs(stats.kurtosis(d)) < 5 * math.sqrt(24 / n)
+    assert stats.kstest(d, "norm").pvalue > 1e-4
+    a = np.abs(d)
+    edges = np.concatenate([[0.0], x[::-1][1:], [np.inf]])  # 0 < x_{R-1} < ... < x_0 < inf
+    counts = np.histogram(a, edges)[0]
+    cdf = special.erf(edges / math.sqrt(2))
+    expect = n * np.diff(cdf)
+    assert stats.chisquare(counts, expect).pvalue > 1e-4
+    tail = a[a > x[0]]
+    assert tail.size == pytest.approx(n * special.erfc(x[0] / math.sqrt(2)), rel=0.15)
+    # conditional tail: P(|g| > s | |g| > x0) = erfc(s/sqrt2) / erfc(x0/sqrt2)
+    assert stats.kstest(tail, lambda s: 1 - special.erfc(s / math.sqrt(2)) /
+                        special.erfc(x[0] / math.sqrt(2))).pvalue > 1e-4
+    assert abs((d > 0).mean() - 0.5) < 5 * 0.5 / math.sqrt(n)
+
+
+def test_normal_policies_draw_from_the_generator_in_row_major_order():
+    """kaimingReluNormal / glorotNormal / normal over L64X128MixRandom: one nextGaussian per
+    element in row-major order, (type)(mean + g * deviation) narrowed once
+    (TensorRandoms.java:615-656); the next draw after the tensor is the generator's next one."""
+    seed = I.builder_step_seed(7, 2)
+    src = I.L64X128MixRandom(seed)
+    w = I.kaiming_relu_normal((3, 5), "FLOAT32", src)
+    ref = I.L64X128MixRandom(seed).gaussian_block(16)
+    std = math.sqrt(2.0 / 5.0)
+    assert np.array_equal(w, (0.0 + ref[:15] * std).astype(np.float32).reshape(3, 5))
+    assert src.next_gaussian() == ref[15]
+    g = I.glorot_normal((4, 2), "FLOAT64", I.L64X128MixRandom(11))
+    ref = I.L64X128MixRandom(11).gaussian_block(8)
+    assert np.array_equal(g, (ref * math.sqrt(2.0 / 6.0)).reshape(4, 2))
+    v = I.initialize((6,), "FLOAT32", I.ParameterInitialization("normal", 1.5, 0.25),
+                     I.L64X128MixRandom(3))
+    assert np.array_equal(v, (1.5 + I.L64X128MixRandom(3).gaussian_block(6) * 0.25).astype(np.float32))
+    # a per-element source gives the same tensor as the block draw
+    class PerElement:
+        def __init__(self, seed):
+            self.g = I.L64X128MixRandom(seed)
+
+        def next_gaussian(self):
+            return self.g.next_gaussian()
+
+    assert np.array_equal(I.kaiming_relu_normal((3, 5), "FLOAT32", PerElement(seed)), w)
+
+
+def test_builder_he_normal_parameters_use_the_step_seeds():
+    from synaptik_amd.training import MlpSpec, init_parameters
+    spec = MlpSpec.chain([6, 4, 3], hidden="relu", loss="ce")
+    Ws, bs = init_parameters(spec, 5, "builder_he_normal")
+    # steps: linear 0, relu 1, linear 2
+    for W, step, fan_in in ((Ws[0], 0, 6), (Ws[1], 2, 4)):
+        ref = I.L64X128MixRandom(I.builder_step_seed(5, step)).gaussian_block(W.size)
+        assert np.array_equal(W, (ref * math.sqrt(2.0 / fan_in)).astype(np.float32).reshape(W.shape))
+    assert all(b is not None and not b.any() for b in bs)

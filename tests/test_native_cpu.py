@@ -119,8 +119,9 @@ def test_optimizer_configuration_validation_mirrors_reference():
 def test_library_exports_the_host_initialization_symbols():
     text = (ROOT / "include" / "synaptik_init.h").read_text()
     names = sorted(set(re.findall(r"\b(shk_lxm_[a-z_0-9]+)\s*\(", text)))
-    assert names == ["shk_lxm_next_double", "shk_lxm_next_long", "shk_lxm_seed",
-                     "shk_lxm_uniform_f32", "shk_lxm_uniform_f64"]
+    assert names == ["shk_lxm_gaussian_tables", "shk_lxm_next_double", "shk_lxm_next_gaussian",
+                     "shk_lxm_next_long", "shk_lxm_seed", "shk_lxm_uniform_f32",
+                     "shk_lxm_uniform_f64"]
     lib = native.load_library()
     for name in names:
         assert hasattr(lib, name), name

@@ -199,22 +199,26 @@ int32_t shk_hip_program_run_static(void* program, uint32_t input_count, void* co
                                    uint32_t output_count, void* const* outputs);
 /* The two-stream step schedule shk_hip_program_create would give an image, without a context or a
  * device (HIP addition, for schedule checks): per step its stream (0 = the context stream, 1 = the
- * side stream) and the one earlier step of the other stream it waits for (-1: none), and the loss
- * MEAN step performed by the run's publication kernel instead of a launch of its own (-1: none).
- * Steps keep program order on each stream; every side step starts after the run's fork from the
- * context stream and the publication follows the join of both. out_steps receives the step count
- * even when `capacity` is too small (INVALID_ARGUMENT). SHK_HIP_CONCURRENT=0 gives the one-stream
- * plan. */
+ * side stream) and the one earlier step of the other stream it waits for (-1: none), and in
+ * out_folded[0..1] the steps the run's last launch performs instead of launches of their own: the
+ * loss MEAN of a fused classifier head and a small staged optimizer pass (-1: none). Steps keep
+ * program order on each stream; every side step starts after the run's fork from the context
+ * stream, and the last launch (folded steps in program order, the trailing step commit, the
+ * status publication) follows the join of both; folded steps and the trailing commit have no
+ * stream entry of their own (stream 0, no wait). out_steps receives the step count even when
+ * `capacity` is too small (INVALID_ARGUMENT). SHK_HIP_CONCURRENT=0 gives the one-stream plan. */
 int32_t shk_hip_program_plan(const void* image, uint64_t image_bytes, uint32_t capacity,
                              uint8_t* out_stream, int32_t* out_wait, int64_t* out_folded,
                              uint32_t* out_steps);
-/* Two-stream step schedule (HIP addition; on by default unless SHK_HIP_CONCURRENT=0 when the
- * program is created): at creation each step's slot reads and writes give its dependencies, and a
- * step that does not depend on the step at the tail of the context stream runs beside it on a
- * second stream of the context (its own reduction scratch), joined back by events -- e.g. the
- * input- and weight-gradient GEMMs of one layer. Results are those of the one-stream order.
- * set_concurrent(0) runs every step on the context stream, (1) restores the plan;
- * side_steps reports how many steps the active plan puts on the second stream. */
+/* Two-stream step schedule (HIP addition; planned at creation unless SHK_HIP_CONCURRENT=0): each
+ * step's slot reads and writes give its dependencies, and a step that does not depend on the step
+ * at the tail of the context stream runs beside it on a second stream of the context (its own
+ * reduction scratch), joined back by events -- e.g. the input- and weight-gradient GEMMs of one
+ * layer. Results are those of the one-stream order. The plan is active by default only for
+ * programs whose GEMMs total at least 2^28 multiply-adds: each cross-stream event costs a few
+ * microseconds on the device, more than overlap gains for smaller programs. set_concurrent(0)
+ * runs every step on the context stream, (1) activates the plan; side_steps reports how many
+ * steps the active plan puts on the second stream. */
 int32_t shk_hip_program_set_concurrent(void* program, int32_t enabled);
 int32_t shk_hip_program_side_steps(void* program, uint32_t* out_steps);
 /* Arena bytes of one lease (internal slots + scratch + status word). */

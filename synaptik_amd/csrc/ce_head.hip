@@ -238,43 +238,10 @@ __global__ void __launch_bounds__(256) ce_head_rows(CeHeadParams p) {
   }
 }
 
-// MEAN of the per-row losses: binary64 partials of rows 4i .. 4i+3 (((l0 + l1) + l2) + l3),
-// summed over i in a 256-strided order and a block tree, then (float)sum / (float)R.
-__device__ __forceinline__ void ce_mean_block(const float* __restrict__ row_loss, int64_t R,
-                                              float* loss, double* dl) {
-  const int64_t P = (R + 3) / 4;
-  double s = 0.0;
-  for (int64_t i = threadIdx.x; i < P; i += 256) {
-    double q[4];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) q[w] = 4 * i + w < R ? (double)row_loss[4 * i + w] : 0.0;
-    s += ((q[0] + q[1]) + q[2]) + q[3];
-  }
-  s = block_sum<256>(s, dl);
-  if (threadIdx.x == 0) loss[0] = (float)s / (float)(double)R;
-}
-
 __global__ void __launch_bounds__(256) ce_head_finish(const float* __restrict__ row_loss, int64_t R,
                                                       float* loss) {
   __shared__ double dl[4];
   ce_mean_block(row_loss, R, loss, dl);
-}
-
-// The same MEAN as the last launch of a run, which then publishes the run's status word: the
-// step commit when a counter is given (it advances when the word is clear), the copy into the
-// pinned host word, and the clear for the next run (one lane, ordinary vector stores), as the
-// plain publication kernel does.
-__global__ void __launch_bounds__(256) ce_finish_publish(const float* __restrict__ row_loss,
-                                                         int64_t R, float* loss, uint32_t* status,
-                                                         uint32_t* host_word, int64_t* counter) {
-  __shared__ double dl[4];
-  ce_mean_block(row_loss, R, loss, dl);
-  if (threadIdx.x == 0) {
-    const uint32_t v = status[0];
-    if (counter != nullptr && v == 0u) counter[0] = counter[0] + 1;
-    host_word[0] = v;
-    status[0] = 0u;
-  }
 }
 
 template <typename T, bool LDSW>
@@ -306,14 +273,6 @@ hipError_t launch_ce_head(const CeHeadParams& in, hipStream_t s) {
           ((reinterpret_cast<uintptr_t>(p.H) | reinterpret_cast<uintptr_t>(p.W) |
             reinterpret_cast<uintptr_t>(p.dx)) & 15u) == 0;
   return p.target_is_64 ? launch_rows<int64_t>(p, s) : launch_rows<int32_t>(p, s);
-}
-
-hipError_t launch_ce_finish_publish(const float* row_loss, int64_t R, float* loss, uint32_t* status,
-                                   uint32_t* host_word, int64_t* commit_counter, hipStream_t s) {
-  if (R <= 0) return launch_status_publish(status, host_word, commit_counter, s);
-  hipLaunchKernelGGL(ce_finish_publish, dim3(1), dim3(256), 0, s, row_loss, R, loss, status,
-                     host_word, commit_counter);
-  return hipGetLastError();
 }
 
 hipError_t launch_ce_head_finish(const float* row_loss, int64_t R, float* loss, hipStream_t s) {

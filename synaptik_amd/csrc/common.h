@@ -141,4 +141,20 @@ __device__ __forceinline__ float block_max(float v, float* lds) {
   return r;
 }
 
+// MEAN of the per-row losses: binary64 partials of rows 4i .. 4i+3 (((l0 + l1) + l2) + l3),
+// summed over i in a 256-strided order and a block tree, then (float)sum / (float)R.
+__device__ __forceinline__ void ce_mean_block(const float* __restrict__ row_loss, int64_t R,
+                                              float* loss, double* dl) {
+  const int64_t P = (R + 3) / 4;
+  double s = 0.0;
+  for (int64_t i = threadIdx.x; i < P; i += 256) {
+    double q[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) q[w] = 4 * i + w < R ? (double)row_loss[4 * i + w] : 0.0;
+    s += ((q[0] + q[1]) + q[2]) + q[3];
+  }
+  s = block_sum<256>(s, dl);
+  if (threadIdx.x == 0) loss[0] = (float)s / (float)(double)R;
+}
+
 }  // namespace shk

@@ -207,17 +207,6 @@ __global__ void fill_u32_kernel(uint32_t* x, int64_t n, uint32_t v) {
        i += (int64_t)gridDim.x * blockDim.x)
     x[i] = v;
 }
-// Copies a program run's status word into the program's pinned host word and clears the device
-// word for the next run; with a counter, first performs the run's step commit (the counter
-// advances when the word is clear). One lane, ordinary (vector) stores.
-__global__ void status_publish_kernel(uint32_t* status, uint32_t* host_word, int64_t* counter) {
-  if (threadIdx.x == 0) {
-    const uint32_t v = status[0];
-    if (counter != nullptr && v == 0u) counter[0] = counter[0] + 1;
-    host_word[0] = v;
-    status[0] = 0u;
-  }
-}
 // One float4 per thread, streamed past the caches: many short workgroups keep the most bytes
 // in flight per CU (measured on MI355X: 6.7 TB/s for a 1 GiB copy, against 5.2-5.8 TB/s for
 // grid-stride loops and 5.2 TB/s for a device-to-device hipMemcpy).
@@ -550,12 +539,6 @@ hipError_t launch_fill(float* x, int64_t n, float value, hipStream_t s) {
 hipError_t launch_fill_u32(uint32_t* x, int64_t n, uint32_t value, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(n, 4)), dim3(256), 0, s, x, n, value);
-  return hipGetLastError();
-}
-hipError_t launch_status_publish(uint32_t* status, uint32_t* host_word, int64_t* commit_counter,
-                                 hipStream_t s) {
-  hipLaunchKernelGGL(status_publish_kernel, dim3(1), dim3(64), 0, s, status, host_word,
-                     commit_counter);
   return hipGetLastError();
 }
 hipError_t launch_copy(const float* src, float* dst, int64_t n, hipStream_t s) {

@@ -83,33 +83,42 @@ __device__ __forceinline__ void epilogue_store4(const GemmParams& p, int64_t row
 // unconditional (indices clamped into range); only terms k < K enter the sum, in order
 // k = 0, 1, ... (fmaf). With p.colsum_partial set, the block also sums the stored values of its
 // rows per column (binary64; waves added in order through LDS) into colsum_partial[y][N].
+//
+// CPL is the columns per lane: 4 (a block covers 256 columns, 16-byte accesses when aligned) or,
+// for narrow outputs (N <= SMALL_K_NARROW_N), 1 (a block covers 64 columns, every lane of a wave
+// has a column of its own, so an expensive epilogue -- the binary64 activation -- is spread over
+// four times the lanes). Each output's sum, its epilogue and the blocks' rows (hence the
+// column-sum partials) do not depend on CPL: both give identical results.
 constexpr int SK_RB = 4;  // rows per wave batch; SK_RB * 16 <= 64 lanes hold a batch's A values
-template <int KB>
+constexpr int64_t SMALL_K_NARROW_N = 128;
+template <int KB, int CPL>
 __global__ void __launch_bounds__(256) gemm_small_k(GemmParams p, int vec_b, int vec_io) {
-  __shared__ double csum[4][256];
+  __shared__ double csum[4][64 * CPL];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t c0 = ((int64_t)blockIdx.x * 64 + lane) * 4;
+  const int64_t c0 = ((int64_t)blockIdx.x * 64 + lane) * CPL;
   bool ok;
   const UpdateCtx uc = begin_update(p, ok);
   const int K = (int)p.K;
   const bool want_sum = p.colsum_partial != nullptr;
-  double cs[4] = {0.0, 0.0, 0.0, 0.0};
+  double cs[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) cs[c] = 0.0;
   // Every lane runs the row loop, also lanes whose columns lie beyond N (their operand reads
   // are clamped into range and they store nothing): the A values of a batch are loaded by
   // lanes 0 .. SK_RB*KB-1 and read back from them with v_readlane.
   {
-    float b[KB][4];
+    float b[KB][CPL];
     const bool full = c0 + 3 < p.N;
-    const bool v4 = vec_io && full;
+    const bool v4 = CPL == 4 && vec_io && full;
 #pragma unroll
     for (int k = 0; k < KB; ++k) {
       const int64_t kk = k < K ? k : K - 1;
-      if (vec_b && full) {
+      if (CPL == 4 && vec_b && full) {
         const float4 t = *reinterpret_cast<const float4*>(p.B + kk * p.ldb + c0);
-        b[k][0] = t.x; b[k][1] = t.y; b[k][2] = t.z; b[k][3] = t.w;
+        b[k][0] = t.x; b[k][1 % CPL] = t.y; b[k][2 % CPL] = t.z; b[k][3 % CPL] = t.w;
       } else {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < CPL; ++c) {
           const int64_t col = min(c0 + c, p.N - 1);
           b[k][c] = p.transB ? p.B[col * p.ldb + kk] : p.B[kk * p.ldb + col];
         }
@@ -144,7 +153,7 @@ __global__ void __launch_bounds__(256) gemm_small_k(GemmParams p, int vec_b, int
         if (r >= p.M) break;
         float acc[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < CPL; ++c) {
           // from +0, as the reference's sum starts (CpuMatmulReferenceKernel.java:34-119): a
           // first product of -0 must not leave the result -0
           float sum = fmaf(a[i][0], b[0][c], 0.0f);
@@ -159,11 +168,11 @@ __global__ void __launch_bounds__(256) gemm_small_k(GemmParams p, int vec_b, int
           epilogue_store4(p, r, c0, acc, y[i]);
           if (want_sum) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) cs[c] += (double)acc[c];
+            for (int c = 0; c < CPL; ++c) cs[c] += (double)acc[c];
           }
         } else {
 #pragma unroll
-          for (int c = 0; c < 4; ++c) {
+          for (int c = 0; c < CPL; ++c) {
             if (c0 + c < p.N) {
               ok &= epilogue_store(p, uc, r, c0 + c, acc[c]);
               if (want_sum) cs[c] += (double)p.C[r * p.ldc + c0 + c];
@@ -175,10 +184,10 @@ __global__ void __launch_bounds__(256) gemm_small_k(GemmParams p, int vec_b, int
   }
   if (want_sum) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) csum[w][lane * 4 + c] = cs[c];
+    for (int c = 0; c < CPL; ++c) csum[w][lane * CPL + c] = cs[c];
     __syncthreads();
-    const int64_t col = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (col < p.N)
+    const int64_t col = (int64_t)blockIdx.x * 64 * CPL + threadIdx.x;
+    if (threadIdx.x < 64 * CPL && col < p.N)
       p.colsum_partial[(int64_t)blockIdx.y * p.N + col] =
           ((csum[0][threadIdx.x] + csum[1][threadIdx.x]) + csum[2][threadIdx.x]) +
           csum[3][threadIdx.x];
@@ -386,8 +395,12 @@ template <int KB>
 struct SmallK {
   static hipError_t run(const GemmParams& p, int vec_b, int vec_io, hipStream_t s) {
     const int64_t y = small_k_row_blocks(p.M, p.N);
-    hipLaunchKernelGGL((gemm_small_k<KB>), dim3((unsigned)((p.N + 255) / 256), (unsigned)y),
-                       dim3(256), 0, s, p, vec_b, vec_io);
+    if (p.N <= SMALL_K_NARROW_N)
+      hipLaunchKernelGGL((gemm_small_k<KB, 1>), dim3((unsigned)((p.N + 63) / 64), (unsigned)y),
+                         dim3(256), 0, s, p, vec_b, vec_io);
+    else
+      hipLaunchKernelGGL((gemm_small_k<KB, 4>), dim3((unsigned)((p.N + 255) / 256), (unsigned)y),
+                         dim3(256), 0, s, p, vec_b, vec_io);
     g_colsum_rows = y;
     return hipGetLastError();
   }

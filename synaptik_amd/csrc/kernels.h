@@ -141,9 +141,6 @@ struct CeHeadParams {
 hipError_t launch_ce_head(const CeHeadParams& p, hipStream_t s);
 // loss[0] = MEAN of row_loss[0 .. R) (binary64 sum, one rounding, divided by R).
 hipError_t launch_ce_head_finish(const float* row_loss, int64_t R, float* loss, hipStream_t s);
-// launch_ce_head_finish followed by launch_status_publish, as one launch
-hipError_t launch_ce_finish_publish(const float* row_loss, int64_t R, float* loss, uint32_t* status,
-                                   uint32_t* host_word, int64_t* commit_counter, hipStream_t s);
 
 // Interpreted fused elementwise chain (see pointwise.hip for the instruction set).
 struct PwInstr {
@@ -192,15 +189,31 @@ struct OptParams {
   uint32_t* status;
 };
 hipError_t launch_optimizer(const OptParams& p, hipStream_t s);
+// Blocks of 1024 elements that launch_optimizer would run for `p` (no launch).
+int64_t optimizer_blocks(const OptParams& p);
+// The last launch of a run, one workgroup: the program's folded trailing steps in program order
+// -- the loss MEAN of a fused classifier head (ce_mean: row_loss[0 .. R) into loss[0], when
+// R > 0) and a staged optimizer pass of at most RUN_FINALE_MAX_OPT_BLOCKS blocks (opt_count > 0),
+// each with the arithmetic of its own kernel -- then the status publication: the step commit
+// when a counter is given (it advances when the word is clear), the copy into the pinned host
+// word and the clear for the next run.
+constexpr int64_t RUN_FINALE_MAX_OPT_BLOCKS = 8;
+struct RunFinale {
+  const float* row_loss;
+  int64_t R;
+  float* loss;
+  int mean_first;  // the MEAN precedes the optimizer pass in program order
+  OptParams opt;   // opt.count == 0: no optimizer pass
+  uint32_t* status;
+  uint32_t* host_word;
+  int64_t* counter;
+};
+hipError_t launch_run_finale(const RunFinale& f, hipStream_t s);
 // Increments the completed-step counter when the status word is clear.
 hipError_t launch_step_commit(int64_t* counter, const uint32_t* status, hipStream_t s);
 
 hipError_t launch_fill(float* x, int64_t n, float value, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* x, int64_t n, uint32_t value, hipStream_t s);
-// Copies a run's status word to pinned host memory and clears it (the last launch of a run);
-// a non-null commit_counter first gets the step commit (incremented when the word is clear).
-hipError_t launch_status_publish(uint32_t* status, uint32_t* host_word, int64_t* commit_counter,
-                                 hipStream_t s);
 hipError_t launch_copy(const float* src, float* dst, int64_t n, hipStream_t s);
 // Canonical publication geometry of a strided view (element units, row-major ordinals).
 constexpr int CANONICAL_MAX_RANK = 16;

@@ -59,14 +59,16 @@ __device__ void accumulation_block(const OptParams& p, const OptTensor& T, int64
   }
 }
 
-__global__ void __launch_bounds__(OPT_NT) optimizer_kernel(OptParams p) {
+// Block `block` of the optimizer pass (OPT_NT threads; no block barrier, so a workgroup may run
+// several blocks one after the other with identical results).
+__device__ __forceinline__ void optimizer_block(const OptParams& p, int64_t block) {
   // Tensor of this block: the table holds each tensor's first block index in `start`.
   int t = 0;
   for (int i = 1; i < p.count; ++i)
-    if ((int64_t)blockIdx.x >= p.t[i].start) t = i;
+    if (block >= p.t[i].start) t = i;
   const OptTensor T = p.t[t];
   if (p.kind >= 3) {
-    accumulation_block(p, T, ((int64_t)blockIdx.x - T.start) * OPT_CHUNK);
+    accumulation_block(p, T, (block - T.start) * OPT_CHUNK);
     return;
   }
   if (p.phase == 1 && *(volatile const uint32_t*)p.status != 0u) return;
@@ -74,7 +76,7 @@ __global__ void __launch_bounds__(OPT_NT) optimizer_kernel(OptParams p) {
   const bool first = completed == 0;
   Coeffs k{1.0f, 1.0f, 1.0f, true};
   if (p.kind != 0) k = adam_coeffs(p, completed + 1);
-  const int64_t base = ((int64_t)blockIdx.x - T.start) * OPT_CHUNK;
+  const int64_t base = (block - T.start) * OPT_CHUNK;
   bool ok = k.ok;
   // Each thread owns 4 consecutive elements: 128-bit streaming loads and stores when all 4 exist
   // and every pointer is 16-byte aligned (device allocations and arena slots are), scalar
@@ -133,21 +135,69 @@ __global__ void __launch_bounds__(OPT_NT) optimizer_kernel(OptParams p) {
   }
 }
 
+__global__ void __launch_bounds__(OPT_NT) optimizer_kernel(OptParams p) {
+  optimizer_block(p, (int64_t)blockIdx.x);
+}
+
+// The run's last launch (RunFinale): folded steps in program order, then the publication. The
+// optimizer blocks run one after the other in this workgroup with their kernel's arithmetic;
+// their failure flags are OR-ed into the status word by device-scope atomics, which the fence
+// and barrier order before lane 0 reads the word back at device scope.
+__global__ void __launch_bounds__(OPT_NT) run_finale_kernel(RunFinale f) {
+  __shared__ double dl[OPT_NT / 64];
+  if (f.R > 0 && f.mean_first) ce_mean_block(f.row_loss, f.R, f.loss, dl);
+  if (f.opt.count > 0) {
+    int64_t blocks = 0;
+    for (int i = 0; i < f.opt.count; ++i) blocks += (f.opt.t[i].n + OPT_CHUNK - 1) / OPT_CHUNK;
+    for (int64_t b = 0; b < blocks; ++b) optimizer_block(f.opt, b);
+  }
+  if (f.R > 0 && !f.mean_first) ce_mean_block(f.row_loss, f.R, f.loss, dl);
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t v = atomicOr(f.status, 0u);  // the word as the device's atomics left it
+    if (f.counter != nullptr && v == 0u) f.counter[0] = f.counter[0] + 1;
+    f.host_word[0] = v;
+    f.status[0] = 0u;
+  }
+}
+
 __global__ void step_commit_kernel(int64_t* counter, const uint32_t* status) {
   if (threadIdx.x == 0 && blockIdx.x == 0 && *status == 0u) *counter = *counter + 1;
 }
 
 }  // namespace
 
-hipError_t launch_optimizer(const OptParams& in, hipStream_t s) {
-  OptParams p = in;
+namespace {
+// Fills each tensor's first block index; returns the block count.
+int64_t assign_blocks(OptParams& p) {
   int64_t blocks = 0;
   for (int i = 0; i < p.count; ++i) {
     p.t[i].start = blocks;
     blocks += (p.t[i].n + OPT_CHUNK - 1) / OPT_CHUNK;
   }
+  return blocks;
+}
+}  // namespace
+
+int64_t optimizer_blocks(const OptParams& in) {
+  OptParams p = in;
+  return assign_blocks(p);
+}
+
+hipError_t launch_optimizer(const OptParams& in, hipStream_t s) {
+  OptParams p = in;
+  const int64_t blocks = assign_blocks(p);
   if (blocks == 0) return hipSuccess;
   hipLaunchKernelGGL(optimizer_kernel, dim3((unsigned)blocks), dim3(OPT_NT), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_run_finale(const RunFinale& in, hipStream_t s) {
+  RunFinale f = in;
+  if (f.opt.count > 0 && assign_blocks(f.opt) > RUN_FINALE_MAX_OPT_BLOCKS)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(run_finale_kernel, dim3(1), dim3(OPT_NT), 0, s, f);
   return hipGetLastError();
 }
 

@@ -263,9 +263,14 @@ struct Program {
   uint32_t side_steps = 0;
   std::vector<uint8_t> stream_of, record_after;
   std::vector<std::vector<uint32_t>> wait_for;
-  // A classifier-loss MEAN step (OP_CE_HEAD finish) that no later step depends on: unprofiled
-  // runs perform it in the run's publication kernel instead of a launch of its own (-1: none).
+  // Trailing steps that no later launched step depends on, performed by the run's last launch
+  // (the publication kernel) in unprofiled runs instead of launches of their own (-1: none): a
+  // classifier-loss MEAN (OP_CE_HEAD finish) and a small staged optimizer pass.
   int64_t folded_finish = -1;
+  int64_t folded_opt = -1;
+  bool folded(size_t j) const {
+    return (int64_t)j == folded_finish || (int64_t)j == folded_opt;
+  }
   // ---- settings and the lease pool, guarded by `mutex` ----
   std::mutex mutex;
   std::condition_variable lease_freed;
@@ -709,8 +714,36 @@ int32_t validate_step(const std::vector<SlotRecord>& slots, size_t idx, const St
 struct Bound {
   std::vector<void*> ptr;  // device pointer per slot
   template <typename T>
-  T* get(int32_t s) const { return s < 0 ? nullptr : static_cast<T*>(ptr[s]); }
+  T* get(int32_t s) const {
+    return s < 0 || (size_t)s >= ptr.size() ? nullptr : static_cast<T*>(ptr[s]);
+  }
 };
+
+// The optimizer launch parameters of an OP_OPTIMIZER step over the bound slots (null pointers
+// for an empty binding: the tensor counts alone).
+shk::OptParams optimizer_params(const Step& st, const Bound& b, uint32_t* status) {
+  const StepRecord& r = st.rec;
+  const int64_t* a = r.iarg;
+  shk::OptParams p{};
+  const OptEntry* e = reinterpret_cast<const OptEntry*>(st.payload.data());
+  p.count = (int)(st.payload.size() / sizeof(OptEntry));
+  for (int i = 0; i < p.count; ++i) {
+    p.t[i].p = b.get<float>(e[i].p);
+    p.t[i].g = b.get<const float>(e[i].g);
+    p.t[i].m = b.get<float>(e[i].m);
+    p.t[i].v = b.get<float>(e[i].v);
+    p.t[i].pn = b.get<float>(e[i].pn);
+    p.t[i].mn = b.get<float>(e[i].mn);
+    p.t[i].vn = b.get<float>(e[i].vn);
+    p.t[i].n = e[i].n;
+  }
+  p.kind = (int)a[0]; p.phase = (int)a[1]; p.nesterov = (int)a[2]; p.has_momentum_slot = (int)a[3];
+  p.lr = r.farg[0]; p.momentum = r.farg[1]; p.dampening = r.farg[2]; p.weight_decay = r.farg[3];
+  p.beta1 = r.farg[4]; p.beta2 = r.farg[5]; p.eps = r.farg[6];
+  p.completed_steps = b.get<const int64_t>(r.slot[0]);
+  p.status = status;
+  return p;
+}
 
 hipError_t enqueue_step(const Step& st, const Bound& b, hipStream_t stream, double* scratch,
                         uint32_t* status) {
@@ -800,27 +833,8 @@ hipError_t enqueue_step(const Step& st, const Bound& b, hipStream_t stream, doub
       p.g = r.farg[0];
       return shk::launch_ce_head(p, stream);
     }
-    case OP_OPTIMIZER: {
-      shk::OptParams p{};
-      const OptEntry* e = reinterpret_cast<const OptEntry*>(st.payload.data());
-      p.count = (int)(st.payload.size() / sizeof(OptEntry));
-      for (int i = 0; i < p.count; ++i) {
-        p.t[i].p = b.get<float>(e[i].p);
-        p.t[i].g = b.get<const float>(e[i].g);
-        p.t[i].m = b.get<float>(e[i].m);
-        p.t[i].v = b.get<float>(e[i].v);
-        p.t[i].pn = b.get<float>(e[i].pn);
-        p.t[i].mn = b.get<float>(e[i].mn);
-        p.t[i].vn = b.get<float>(e[i].vn);
-        p.t[i].n = e[i].n;
-      }
-      p.kind = (int)a[0]; p.phase = (int)a[1]; p.nesterov = (int)a[2]; p.has_momentum_slot = (int)a[3];
-      p.lr = r.farg[0]; p.momentum = r.farg[1]; p.dampening = r.farg[2]; p.weight_decay = r.farg[3];
-      p.beta1 = r.farg[4]; p.beta2 = r.farg[5]; p.eps = r.farg[6];
-      p.completed_steps = b.get<const int64_t>(s[0]);
-      p.status = status;
-      return shk::launch_optimizer(p, stream);
-    }
+    case OP_OPTIMIZER:
+      return shk::launch_optimizer(optimizer_params(st, b, status), stream);
     case OP_STEP_COMMIT:
       return shk::launch_step_commit(b.get<int64_t>(s[0]), status, stream);
     case OP_FILL:
@@ -927,37 +941,62 @@ bool large_gemm(const Step& st) {
   return macs >= (double)(1ll << 28);
 }
 
-// The last OP_CE_HEAD finish step whose accesses conflict with no later step's (nothing later
-// reads the loss it writes or writes what it reads), so it can move to the end of the run.
-// SHK_HIP_FOLD_FINISH=0 keeps it a launch of its own.
+// Whether the two-stream plan is active by default: only for programs whose GEMMs total at
+// least 2^28 multiply-adds. Each cross-stream event costs a few microseconds on the device
+// (measured on MI355X: a 16 -> 64 -> 1 training step, 12 small kernels, takes 61 us on one stream
+// and 80 us on two), which only steps long enough to hide side work beside them repay.
+bool side_stream_pays(const Program& pr) {
+  double macs = 0.0;
+  for (const Step& st : pr.steps)
+    if (st.rec.opcode == OP_GEMM) {
+      const int64_t* a = st.rec.iarg;
+      if (a[0] > 0 && a[1] > 0 && a[2] > 0) macs += (double)a[0] * (double)a[1] * (double)a[2];
+    }
+  return macs >= (double)(1ll << 28);
+}
+
+// Folding: the last OP_CE_HEAD finish step, and the last staged optimizer pass (phase 2, SGD /
+// Adam / AdamW) of at most RUN_FINALE_MAX_OPT_BLOCKS blocks, whose accesses conflict with no
+// later launched step's (nothing later reads what they write or writes what they read) move to
+// the run's last launch, which performs them in program order after every launched step. Runs
+// before plan_streams, which leaves folded steps out of the schedule. SHK_HIP_FOLD_FINISH=0 keeps
+// every step a launch of its own.
 void plan_fold(Program* pr) {
   static const bool on = [] {
     const char* e = std::getenv("SHK_HIP_FOLD_FINISH");
     return !(e != nullptr && e[0] == '0');
   }();
   pr->folded_finish = -1;
+  pr->folded_opt = -1;
   const size_t n = pr->steps.size();
   const size_t launched = n > 0 && pr->steps[n - 1].rec.opcode == OP_STEP_COMMIT ? n - 1 : n;
   if (!on) return;
-  for (size_t j = launched; j-- > 0;) {
-    const StepRecord& r = pr->steps[j].rec;
-    if (r.opcode != OP_CE_HEAD || r.iarg[4] != 1) continue;
-    const Access aj = step_access(pr->steps[j]);
-    for (size_t k = j + 1; k < launched; ++k)
-      if (accesses_conflict(aj, step_access(pr->steps[k]))) return;
-    pr->folded_finish = (int64_t)j;
-    break;
-  }
-  // The folded step is never launched, so no event may be recorded after it and no step may
-  // wait for it: a capture would then wait on an event that was never recorded in it. plan_streams
-  // gives it no such edge when no later step conflicts with it (the same accesses_conflict);
-  // should the two ever disagree, the step stays a launch of its own.
-  const int64_t f = pr->folded_finish;
-  if (f < 0) return;
-  bool edge = f < (int64_t)pr->record_after.size() && pr->record_after[(size_t)f] != 0;
-  for (const auto& w : pr->wait_for)
-    for (uint32_t i : w) edge |= (int64_t)i == f;
-  if (edge) pr->folded_finish = -1;
+  auto last_foldable = [&](auto eligible) -> int64_t {
+    for (size_t j = launched; j-- > 0;) {
+      if (!eligible(pr->steps[j])) continue;
+      const Access aj = step_access(pr->steps[j]);
+      for (size_t k = j + 1; k < launched; ++k)
+        if (!pr->folded(k) && accesses_conflict(aj, step_access(pr->steps[k]))) return -1;
+      return (int64_t)j;
+    }
+    return -1;
+  };
+  static const int64_t max_elements = [] {
+    const char* e = std::getenv("SHK_HIP_FOLD_OPT_MAX");
+    return e != nullptr ? std::atoll(e) : (int64_t)1024;
+  }();
+  pr->folded_opt = last_foldable([](const Step& st) {
+    const StepRecord& r = st.rec;
+    if (r.opcode != OP_OPTIMIZER || r.iarg[1] != 2 || r.iarg[0] > 2) return false;
+    const shk::OptParams p = optimizer_params(st, Bound(), nullptr);
+    int64_t elements = 0;
+    for (int i = 0; i < p.count; ++i) elements += p.t[i].n;
+    return elements <= max_elements &&
+           shk::optimizer_blocks(p) <= shk::RUN_FINALE_MAX_OPT_BLOCKS;
+  });
+  pr->folded_finish = last_foldable([](const Step& st) {
+    return st.rec.opcode == OP_CE_HEAD && st.rec.iarg[4] == 1;
+  });
 }
 
 void plan_streams(Program* pr) {
@@ -970,12 +1009,16 @@ void plan_streams(Program* pr) {
   std::vector<Access> acc(n);
   for (size_t j = 0; j < n; ++j) acc[j] = step_access(pr->steps[j]);
   int64_t tail0 = -1;
+  const size_t launched = pr->steps[n - 1].rec.opcode == OP_STEP_COMMIT ? n - 1 : n;
   // per stream: the latest step of the other stream its tail already follows (through a wait)
   int64_t covered[2] = {-1, -1};
   for (size_t j = 0; j < n; ++j) {
+    // steps the publication kernel performs (folded ones, the trailing commit) follow the join
+    // of both streams: they take no part in the schedule
+    if (j >= launched || pr->folded(j)) continue;
     std::vector<uint32_t> deps;
     for (size_t i = 0; i < j; ++i)
-      if (accesses_conflict(acc[i], acc[j])) deps.push_back((uint32_t)i);
+      if (!pr->folded(i) && accesses_conflict(acc[i], acc[j])) deps.push_back((uint32_t)i);
     bool on_tail0 = tail0 < 0;
     for (uint32_t i : deps) on_tail0 |= (int64_t)i == tail0;
     // A large GEMM stays on the context stream even when it could run beside the chain: two
@@ -1013,20 +1056,29 @@ hipError_t enqueue_steps(const Program& pr, Lease& ls, const Bound& b, hipStream
   if (n > 0 && pr.steps[n - 1].rec.opcode == OP_STEP_COMMIT)
     commit = b.get<int64_t>(pr.steps[n - 1].rec.slot[0]);
   const size_t launched = commit != nullptr ? n - 1 : n;
-  // the loss MEAN folded into the publication (not in profiled runs: their per-step events
+  // folded steps go into the run's last launch (not in profiled runs: their per-step events
   // bracket every step's own launch)
-  const int64_t fold = profile ? -1 : pr.folded_finish;
+  auto skipped = [&](size_t j) { return !profile && pr.folded(j); };
   auto publish = [&]() -> hipError_t {
-    if (fold < 0) return shk::launch_status_publish(ls.status, ls.host_status, commit, s0);
-    const StepRecord& r = pr.steps[(size_t)fold].rec;
-    return shk::launch_ce_finish_publish(b.get<const float>(r.slot[0]), r.iarg[0],
-                                         b.get<float>(r.slot[1]), ls.status, ls.host_status,
-                                         commit, s0);
+    shk::RunFinale f{};
+    f.status = ls.status;
+    f.host_word = ls.host_status;
+    f.counter = commit;
+    if (!profile && pr.folded_finish >= 0) {
+      const StepRecord& r = pr.steps[(size_t)pr.folded_finish].rec;
+      f.row_loss = b.get<const float>(r.slot[0]);
+      f.R = r.iarg[0];
+      f.loss = b.get<float>(r.slot[1]);
+      f.mean_first = pr.folded_opt < 0 || pr.folded_finish < pr.folded_opt;
+    }
+    if (!profile && pr.folded_opt >= 0)
+      f.opt = optimizer_params(pr.steps[(size_t)pr.folded_opt], b, ls.status);
+    return shk::launch_run_finale(f, s0);
   };
   if (!two_streams || profile) {
     for (size_t i = 0; i < n; ++i) {
       if (profile && (e = hipEventRecord(ls.events[i], s0)) != hipSuccess) return e;
-      if (i < launched && (int64_t)i != fold &&
+      if (i < launched && !skipped(i) &&
           (e = enqueue_step(pr.steps[i], b, s0, ls.scratch, ls.status)) != hipSuccess)
         return e;
     }
@@ -1038,7 +1090,7 @@ hipError_t enqueue_steps(const Program& pr, Lease& ls, const Bound& b, hipStream
       (e = hipStreamWaitEvent(s1, ls.fork, 0)) != hipSuccess)
     return e;
   for (size_t j = 0; j < launched; ++j) {
-    if ((int64_t)j == fold) continue;  // no later step waits for it (plan_fold)
+    if (skipped(j)) continue;  // no later step waits for it (plan_fold, plan_streams)
     const bool side = pr.stream_of[j] != 0;
     hipStream_t st = side ? s1 : s0;
     for (uint32_t i : pr.wait_for[j])
@@ -1789,8 +1841,8 @@ int32_t decode_image(const void* image, uint64_t image_bytes, Program* pr) {
   uint64_t off = 256;
   pr->scratch_off = off;
   off += ((scratch_doubles * 8 + 255) / 256) * 256;
-  plan_streams(pr);
   plan_fold(pr);
+  plan_streams(pr);
   pr->scratch_side_off = off;
   if (pr->side_steps > 0) off += ((scratch_doubles * 8 + 255) / 256) * 256;
   pr->internal_offset.assign(h.n_slots, 0);
@@ -1825,8 +1877,8 @@ int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_
       destroy_program(pr);
       return ds;
     }
-    pr->concurrent = pr->side_steps > 0;
-    if (pr->concurrent) {
+    pr->concurrent = pr->side_steps > 0 && side_stream_pays(*pr);
+    if (pr->side_steps > 0) {
       std::lock_guard<std::mutex> lock(c->mutex);
       if (c->side_stream == nullptr &&
           (hipSetDevice(c->device) != hipSuccess ||
@@ -1897,7 +1949,7 @@ int32_t shk_hip_program_plan(const void* image, uint64_t image_bytes, uint32_t c
                              uint8_t* out_stream, int32_t* out_wait, int64_t* out_folded,
                              uint32_t* out_steps) {
   if (out_steps != nullptr) *out_steps = 0;
-  if (out_folded != nullptr) *out_folded = -1;
+  if (out_folded != nullptr) out_folded[0] = out_folded[1] = -1;
   if (image == nullptr || out_steps == nullptr)
     return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "image or out_steps is null");
   try {
@@ -1907,7 +1959,10 @@ int32_t shk_hip_program_plan(const void* image, uint64_t image_bytes, uint32_t c
     if (st != SHK_HIP_STATUS_OK) return st;
     const size_t n = pr.steps.size();
     *out_steps = (uint32_t)n;
-    if (out_folded != nullptr) *out_folded = pr.folded_finish;
+    if (out_folded != nullptr) {
+      out_folded[0] = pr.folded_finish;
+      out_folded[1] = pr.folded_opt;
+    }
     if (capacity < n || out_stream == nullptr || out_wait == nullptr)
       return fail(SHK_HIP_STATUS_INVALID_ARGUMENT, "plan of %zu steps needs that capacity", n);
     for (size_t j = 0; j < n; ++j) {

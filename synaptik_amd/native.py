@@ -267,22 +267,21 @@ def validate_program_image(image: bytes) -> int:
 
 def program_plan(image: bytes):
     """The two-stream schedule program creation gives an image, without a device
-    (`shk_hip_program_plan`): (stream per step, the step each waits for or -1, the loss MEAN step
-    folded into the publication or -1)."""
+    (`shk_hip_program_plan`): (stream per step, the step each waits for or -1, the steps folded
+    into the run's last launch: [loss MEAN or -1, optimizer pass or -1])."""
     lib = load_library()
     buf = ctypes.create_string_buffer(bytes(image), max(1, len(image)))
     n = ctypes.c_uint32()
-    folded = ctypes.c_int64()
-    st = lib.shk_hip_program_plan(buf, len(image), 0, None, None, ctypes.byref(folded),
-                                  ctypes.byref(n))
+    folded = (ctypes.c_int64 * 2)()
+    st = lib.shk_hip_program_plan(buf, len(image), 0, None, None, folded, ctypes.byref(n))
     if n.value == 0:
         check(lib, st)
-        return [], [], -1
+        return [], [], [-1, -1]
     streams = (ctypes.c_uint8 * n.value)()
     waits = (ctypes.c_int32 * n.value)()
-    check(lib, lib.shk_hip_program_plan(buf, len(image), n.value, streams, waits,
-                                        ctypes.byref(folded), ctypes.byref(n)))
-    return list(streams), list(waits), folded.value
+    check(lib, lib.shk_hip_program_plan(buf, len(image), n.value, streams, waits, folded,
+                                        ctypes.byref(n)))
+    return list(streams), list(waits), list(folded)
 
 
 def storage_transfer_bytes(element_width: int, shape, strides, storage_offset: int) -> int:

@@ -15,7 +15,8 @@ synaptik_amd/csrc/*.hip), not from runtime.cpp's step_access:
 The schedule (`native.program_plan`) is then checked as the runtime enqueues it: a fork from
 the context stream before the first step, every step on its stream in program order, one event
 wait per step at most (recorded after the waited-for step), the join of both streams, and the
-publication kernel (which also performs the folded loss MEAN and the trailing step commit).
+run's last launch (which performs the folded steps -- a classifier-loss MEAN, a small staged
+optimizer pass -- in program order, then the trailing step commit and the status publication).
 Every pair of steps whose effects conflict (read-after-write, write-after-read,
 write-after-write, status read against status OR) must be ordered by a happens-before path.
 """
@@ -214,17 +215,21 @@ class Hazard:
         return f"steps {self.first} -> {self.second} unordered: {', '.join(self.reasons)}"
 
 
-def check_plan(steps: list[DecodedStep], stream_of, wait_for, folded: int) -> list[Hazard]:
+def check_plan(steps: list[DecodedStep], stream_of, wait_for, folded=()) -> list[Hazard]:
     """Returns every conflicting pair of steps without a happens-before path under the plan
-    (empty: the schedule is race-free), after checking the plan's own well-formedness."""
+    (empty: the schedule is race-free), after checking the plan's own well-formedness. `folded`:
+    the steps the run's last launch performs (-1 entries ignored)."""
     n = len(steps)
     assert len(stream_of) == n and len(wait_for) == n
     commit_last = n > 0 and steps[-1].opcode == P.OP_STEP_COMMIT
     launched = n - 1 if commit_last else n
-    # publication performs the trailing commit and the folded MEAN after the join
-    in_pub = set([n - 1] if commit_last else []) | ({folded} if folded >= 0 else set())
-    if folded >= 0:
-        assert steps[folded].opcode == P.OP_CE_HEAD and steps[folded].iargs[4] == 1
+    # the last launch performs the folded steps and the trailing commit after the join
+    folded = {int(f) for f in folded if f >= 0}
+    in_pub = set([n - 1] if commit_last else []) | folded
+    for f in folded:
+        st = steps[f]
+        assert (st.opcode == P.OP_CE_HEAD and st.iargs[4] == 1) or \
+            (st.opcode == P.OP_OPTIMIZER and st.iargs[1] == 2 and st.iargs[0] <= 2), f
     for j, w in enumerate(wait_for):
         if w < 0:
             continue

@@ -38,11 +38,8 @@ def test_training_state_identical_with_and_without_side_stream(ctx, dims, loss, 
         s = HipTrainingSession.open(ctx, spec, Ws, bs, opt, B)
         for prog, _ in s._programs.values():
             prog.set_graph_mode(graphs)
-            if concurrent:
-                assert prog.side_steps() > 0
             prog.set_concurrent(concurrent)
-            if not concurrent:
-                assert prog.side_steps() == 0
+            assert (prog.side_steps() > 0) == concurrent
         objs = [s.run(x, y).objective for x, y in batches]
         sessions.append((s, objs))
     (a, oa), (b, ob) = sessions

@@ -201,6 +201,7 @@ def test_failed_two_stream_steps_leave_no_trace(ctx):
     bad = good.copy()
     bad[200] = 10
     a = HipTrainingSession.open(ctx, spec, Ws, bs, Adam(1e-3), 256)
+    a.program.set_concurrent(True)  # a program this small runs on one stream by default
     assert a.program.side_steps() > 0
     for _ in range(2):
         with pytest.raises(HipIndexError):

@@ -355,10 +355,18 @@ __global__ void lse_bwd_kernel(const float* __restrict__ x, const float* __restr
 
 // ---- MSE (CpuLossReferenceKernel.java:67-87, LossGradientRules.java:77-97) ----
 constexpr int MSE_BLOCKS = 1024;
+// MEAN finalization divides the binary32 sum by the exact count before one final rounding.
+__device__ __forceinline__ float mse_loss(double s, int64_t n, int reduction_sum) {
+  const float sf = (float)s;
+  return reduction_sum ? sf : (float)((double)sf / (double)n);
+}
+// Pass 1: block b's binary64 partial sum of squared differences (and the gradient). A launch of
+// one block finishes the loss itself: its partial is the whole sum, which pass 2 would only
+// return unchanged.
 __global__ void __launch_bounds__(256) mse_pass1(const float* __restrict__ p,
                                                  const float* __restrict__ t,
                                                  float* __restrict__ grad, int64_t n, float gn,
-                                                 double* part) {
+                                                 double* part, float* loss, int reduction_sum) {
   __shared__ double dl[4];
   double s = 0.0;
   const int64_t stride = (int64_t)gridDim.x * 256;
@@ -391,7 +399,10 @@ __global__ void __launch_bounds__(256) mse_pass1(const float* __restrict__ p,
     }
   }
   s = block_sum<256>(s, dl);
-  if (threadIdx.x == 0) part[blockIdx.x] = s;
+  if (threadIdx.x == 0) {
+    if (gridDim.x == 1) loss[0] = mse_loss(s, n, reduction_sum);
+    else part[blockIdx.x] = s;
+  }
 }
 __global__ void __launch_bounds__(256) mse_pass2(const double* part, int P, int64_t n,
                                                  int reduction_sum, float* loss) {
@@ -399,11 +410,7 @@ __global__ void __launch_bounds__(256) mse_pass2(const double* part, int P, int6
   double s = 0.0;
   for (int i = threadIdx.x; i < P; i += 256) s += part[i];
   s = block_sum<256>(s, dl);
-  if (threadIdx.x == 0) {
-    // MEAN finalization divides the binary32 sum by the exact count before one final rounding.
-    const float sf = (float)s;
-    loss[0] = reduction_sum ? sf : (float)((double)sf / (double)n);
-  }
+  if (threadIdx.x == 0) loss[0] = mse_loss(s, n, reduction_sum);
 }
 
 // ---- Index categorical cross-entropy (CpuLossReferenceKernel.java:196-218,261-288;
@@ -570,9 +577,11 @@ hipError_t launch_mse(const float* p, const float* t, float* loss, float* grad, 
   const unsigned blocks = (unsigned)std::min<int64_t>(MSE_BLOCKS, std::max<int64_t>(1, (n + 1023) / 1024));
   // restore(g): MEAN divides g by the count (an exact binary32 sum of ones); SUM expands g.
   const float gn = reduction_sum ? g : g / (float)n;
-  hipLaunchKernelGGL(mse_pass1, dim3(blocks), dim3(256), 0, s, p, t, grad, n, gn, partial);
-  hipLaunchKernelGGL(mse_pass2, dim3(1), dim3(256), 0, s, (const double*)partial, (int)blocks, n,
-                     reduction_sum, loss);
+  hipLaunchKernelGGL(mse_pass1, dim3(blocks), dim3(256), 0, s, p, t, grad, n, gn, partial, loss,
+                     reduction_sum);
+  if (blocks > 1)
+    hipLaunchKernelGGL(mse_pass2, dim3(1), dim3(256), 0, s, (const double*)partial, (int)blocks,
+                       n, reduction_sum, loss);
   return hipGetLastError();
 }
 

@@ -143,10 +143,13 @@ __global__ void __launch_bounds__(OPT_NT) optimizer_kernel(OptParams p) {
 // optimizer blocks run one after the other in this workgroup with their kernel's arithmetic;
 // their failure flags are OR-ed into the status word by device-scope atomics, which the fence
 // and barrier order before lane 0 reads the word back at device scope.
+// Instantiated with and without the optimizer pass: a run without one launches a kernel with no
+// optimizer code (and no private memory).
+template <bool OPT>
 __global__ void __launch_bounds__(OPT_NT) run_finale_kernel(RunFinale f) {
   __shared__ double dl[OPT_NT / 64];
   if (f.R > 0 && f.mean_first) ce_mean_block(f.row_loss, f.R, f.loss, dl);
-  if (f.opt.count > 0) {
+  if (OPT && f.opt.count > 0) {
     int64_t blocks = 0;
     for (int i = 0; i < f.opt.count; ++i) blocks += (f.opt.t[i].n + OPT_CHUNK - 1) / OPT_CHUNK;
     for (int64_t b = 0; b < blocks; ++b) optimizer_block(f.opt, b);
@@ -197,7 +200,10 @@ hipError_t launch_run_finale(const RunFinale& in, hipStream_t s) {
   RunFinale f = in;
   if (f.opt.count > 0 && assign_blocks(f.opt) > RUN_FINALE_MAX_OPT_BLOCKS)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(run_finale_kernel, dim3(1), dim3(OPT_NT), 0, s, f);
+  if (f.opt.count > 0)
+    hipLaunchKernelGGL(run_finale_kernel<true>, dim3(1), dim3(OPT_NT), 0, s, f);
+  else
+    hipLaunchKernelGGL(run_finale_kernel<false>, dim3(1), dim3(OPT_NT), 0, s, f);
   return hipGetLastError();
 }
 

@@ -43,7 +43,17 @@ def images():
 def validate(img: bytes) -> int:
     buf = ctypes.create_string_buffer(img, max(1, len(img)))
     arena = ctypes.c_uint64()
-    return lib.shk_hip_program_validate(buf, len(img), ctypes.byref(arena))
+    st = lib.shk_hip_program_validate(buf, len(img), ctypes.byref(arena))
+    # the schedule export decodes the same bytes: capacity probe, then a full plan
+    n = ctypes.c_uint32()
+    folded = (ctypes.c_int64 * 2)()
+    lib.shk_hip_program_plan(buf, len(img), 0, None, None, folded, ctypes.byref(n))
+    if n.value:
+        streams = (ctypes.c_uint8 * n.value)()
+        waits = (ctypes.c_int32 * n.value)()
+        assert lib.shk_hip_program_plan(buf, len(img), n.value, streams, waits, folded,
+                                        ctypes.byref(n)) == st
+    return st
 
 
 def main():
@@ -94,6 +104,9 @@ def main():
     g = L64X128MixRandom(-7)
     g.next_longs(10_000)
     g.uniform_block(-1.0, 1.0, 10_000, np.float32)
+    g.gaussian_block(100_000)  # fast path, overhangs, cap and tail
+    from synaptik_amd.initializers import gaussian_tables
+    gaussian_tables()
     # null and foreign handles
     vp = ctypes.c_void_p
     junk = vp(ctypes.addressof(ctypes.create_string_buffer(512)))
@@ -107,6 +120,7 @@ def main():
     assert lib.shk_hip_program_run(junk, 0, None, 0, None) == 1
     assert lib.shk_hip_program_run_static(junk, 0, None, 0, None) == 1
     assert lib.shk_hip_program_validate(None, 0, None) == 1
+    assert lib.shk_hip_program_plan(None, 0, 0, None, None, None, None) == 1
     for fn in ("shk_hip_program_set_graph_mode", "shk_hip_program_set_concurrent",
                "shk_hip_program_set_profiling"):
         assert getattr(lib, fn)(None, 1) == 1 and getattr(lib, fn)(junk, 0) == 1

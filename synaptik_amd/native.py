@@ -392,6 +392,17 @@ class HipBuffer:
             pass
 
 
+class HipBinding:
+    """Prepared handle arrays of a program run's inputs and outputs (HipProgram.bind)."""
+    __slots__ = ("ins", "outs", "n_in", "n_out", "buffers")
+
+    def __init__(self, inputs, outputs):
+        self.buffers = (tuple(inputs), tuple(outputs))
+        self.n_in, self.n_out = len(inputs), len(outputs)
+        self.ins = (ctypes.c_void_p * max(1, self.n_in))(*[b.handle.value for b in inputs])
+        self.outs = (ctypes.c_void_p * max(1, self.n_out))(*[b.handle.value for b in outputs])
+
+
 class HipProgram:
     """A created program (`shk_hip_program_create`) bound to a context."""
 
@@ -407,6 +418,16 @@ class HipProgram:
         ins = (ctypes.c_void_p * max(1, len(inputs)))(*[b.handle.value for b in inputs])
         outs = (ctypes.c_void_p * max(1, len(outputs)))(*[b.handle.value for b in outputs])
         check(self.lib, self.lib.shk_hip_program_run(self.handle, len(inputs), ins, len(outputs), outs))
+
+    def bind(self, inputs, outputs) -> "HipBinding":
+        """The handle arrays of one set of bindings, built once for repeated runs
+        (`run_bound`); the binding keeps its buffers referenced. The native call validates the
+        bindings on every run as `run` does."""
+        return HipBinding(inputs, outputs)
+
+    def run_bound(self, binding: "HipBinding") -> None:
+        check(self.lib, self.lib.shk_hip_program_run(self.handle, binding.n_in, binding.ins,
+                                                     binding.n_out, binding.outs))
 
     def run_static(self, inputs, outputs) -> None:
         """One run whose per-run device memory is the library's static per-device array

@@ -455,6 +455,7 @@ class HipTrainingSession:
         self.optimizer = optimizer
         self.label_dtype = label_dtype
         self._programs: dict[tuple, tuple[HipProgram, TrainingLayout]] = {}
+        self._bindings: dict[tuple, object] = {}  # prepared handle arrays of the plain step
         self.program, lay = self._program(GradientMode.RESET_AND_STEP, False)
         self.layout = lay
         Ws = [np.asarray(w, np.float32) for w in weights]
@@ -513,16 +514,27 @@ class HipTrainingSession:
     def run_resident(self, x: HipBuffer, y: HipBuffer,
                      mode: str = GradientMode.RESET_AND_STEP) -> None:
         """One run on device-resident batch buffers; the objective stays on the device."""
+        pending = self.accumulated_gradient_runs > 0
+        if mode == GradientMode.RESET_AND_STEP and not pending:
+            # the plain step: its two handle arrays (one per current set) are built once per
+            # batch buffer pair
+            key = (self._cur, x.handle.value, y.handle.value)
+            bound = self._bindings.get(key)
+            prog, _ = self._programs[(mode, False)]
+            if bound is None:
+                cur, nxt = self._sets[self._cur], self._sets[1 - self._cur]
+                bound = prog.bind(cur[0] + cur[1] + cur[2] + cur[3] + nxt[0] + nxt[1] + nxt[2]
+                                  + nxt[3] + [self.counter, x, y], [self.loss])
+                if len(self._bindings) >= 8:
+                    self._bindings.clear()
+                self._bindings[key] = bound
+            prog.run_bound(bound)
+            self._cur = 1 - self._cur
+            return
         cur = self._sets[self._cur]
         nxt = self._sets[1 - self._cur]
         current = cur[0] + cur[1] + cur[2] + cur[3]
         candidate = nxt[0] + nxt[1] + nxt[2] + nxt[3]
-        pending = self.accumulated_gradient_runs > 0
-        if mode == GradientMode.RESET_AND_STEP and not pending:
-            prog, _ = self._programs[(mode, False)]
-            prog.run(current + candidate + [self.counter, x, y], [self.loss])
-            self._cur = 1 - self._cur
-            return
         self._ensure_accumulators()
         prog, _ = self._program(mode, mode == GradientMode.RESET_AND_STEP)
         if mode == GradientMode.ACCUMULATE:
@@ -644,6 +656,7 @@ class HipTrainingSession:
         self.accumulated_gradient_runs = st.accumulated_gradient_runs
 
     def close(self) -> None:
+        self._bindings.clear()
         for prog, _ in self._programs.values():
             prog.close()
         self._programs.clear()

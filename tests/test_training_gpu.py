@@ -11,7 +11,7 @@ import pytest
 from oracle import oracle
 from synaptik_amd.native import HipArithmeticError, HipIndexError
 from synaptik_amd.training import (Adam, AdamW, Dense, HipTrainingSession, MlpSpec, Sgd,
-                                   init_parameters)
+                                   init_parameters, lower_training_step)
 from tests.conftest import needs_two_streams
 
 pytestmark = pytest.mark.gpu
@@ -216,5 +216,56 @@ def test_failed_two_stream_steps_leave_no_trace(ctx):
                     sb.weights + sb.biases + sb.first + sb.second):
         assert np.array_equal(p.view(np.uint32), q.view(np.uint32))
     assert a.objective().view(np.uint32) == b.objective().view(np.uint32)
+    a.close()
+    b.close()
+
+
+def test_failure_of_the_folded_bias_update_alone_commits_nothing(ctx):
+    """Zero inputs and zero biases make every weight gradient exactly zero (the hidden ReLU is
+    off, its gradient masked to zero), while the output bias gradient under MSE SUM, the column
+    sum of 32 rows of 2 * (0 - 1.5e38), overflows: only the bias update, which the run's last
+    launch performs (a program this small folds it), flags the status word. The run raises
+    ArithmeticError and commits nothing -- the last launch reads the word after its own update
+    -- in the folded form and in the profiled form that launches the update on its own."""
+    from synaptik_amd.native import program_plan
+    spec = MlpSpec(MlpSpec.chain([4, 8, 1], hidden="relu").layers, "mse", "sum")
+    Ws, bs = init_parameters(spec, 0, "he_normal")
+    pb, _ = lower_training_step(spec, 32, Sgd(0.1))
+    assert program_plan(pb.image())[2][1] >= 0  # the bias update is folded
+    x = np.zeros((32, 4), np.float32)
+    bad = np.full((32, 1), 1.5e38, np.float32)
+    for profiled in (False, True):
+        sess = HipTrainingSession.open(ctx, spec, Ws, bs, Sgd(0.1), 32)
+        sess.program.set_profiling(profiled)
+        before = sess.state()
+        with pytest.raises(HipArithmeticError):
+            sess.run(x, bad)
+        after = sess.state()
+        assert after.optimizer_steps == before.optimizer_steps == 0, profiled
+        for a, b in zip(before.weights + before.biases, after.weights + after.biases):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), profiled
+        sess.run(x, np.zeros((32, 1), np.float32))
+        assert sess.optimizer_steps == 1
+        sess.close()
+
+
+def test_folded_bias_update_matches_its_own_launch(ctx):
+    """The C1 network's bias update runs in the run's last launch; profiled runs launch it on its
+    own. Five steps of each give bit-identical objectives, parameters and counters."""
+    spec = MlpSpec.chain([16, 64, 1], hidden="tanh", loss="mse")
+    Ws, bs = init_parameters(spec, 0, "builder")
+    rng = np.random.default_rng(2)
+    a = HipTrainingSession.open(ctx, spec, Ws, bs, Sgd(0.01), 256)
+    b = HipTrainingSession.open(ctx, spec, Ws, bs, Sgd(0.01), 256)
+    b.program.set_profiling(True)
+    for step in range(5):
+        x = rng.standard_normal((256, 16)).astype(np.float32)
+        y = rng.standard_normal((256, 1)).astype(np.float32)
+        oa, ob = a.run(x, y).objective, b.run(x, y).objective
+        assert np.float32(oa).view(np.uint32) == np.float32(ob).view(np.uint32), step
+    sa, sb = a.state(), b.state()
+    assert sa.optimizer_steps == sb.optimizer_steps == 5
+    for u, v in zip(sa.weights + sa.biases, sb.weights + sb.biases):
+        assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
     a.close()
     b.close()

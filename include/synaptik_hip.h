@@ -235,8 +235,9 @@ int32_t shk_hip_program_step_count(void* program, uint32_t* out_steps);
 /* HIP-graph replay of the whole step sequence: each distinct set of bound buffers is captured
  * once and replayed with one launch. The default is on, except for a program whose every step
  * is a GEMM large enough to occupy the device (at least 2^28 multiply-adds): there the launches
- * are hidden behind the previous kernel anyway and replay only adds per-node cost.
- * SHK_HIP_GRAPHS=0 turns the default off. Profiled runs always launch step by step. */
+ * are hidden behind the previous kernel anyway and replay only adds per-node cost; and for a
+ * program of at most five launched steps, whose direct launches cost less than a replay's
+ * fixed cost. SHK_HIP_GRAPHS=0 turns the default off. Profiled runs always launch step by step. */
 int32_t shk_hip_program_set_graph_mode(void* program, int32_t enabled);
 /* The current graph-replay setting (HIP addition). */
 int32_t shk_hip_program_graph_mode(void* program, int32_t* out_enabled);

@@ -1910,12 +1910,20 @@ int32_t shk_hip_program_create(void* context, const void* image, uint64_t image_
     pr->step_ms.assign(pr->steps.size(), 0.0);
     {
       const char* g = getenv("SHK_HIP_GRAPHS");
-      // a program of large GEMMs only launches step by step by default: each launch is hidden
+      // A program of large GEMMs only launches step by step by default: each launch is hidden
       // behind the previous kernel, and graph replay adds a few microseconds per node (C2's
-      // fused layer: 0.404 ms direct, 0.410 ms replayed)
+      // fused layer: 0.404 ms direct, 0.410 ms replayed). So does a program of at most five
+      // launched steps: a synchronous run replayed as a graph costs about 30 us whatever its
+      // length up to 16 kernels, launched directly about 14 us plus 2.5 us per kernel (measured
+      // on MI355X with chains of 1 to 16 copy steps: 16 / 22 / 27 / 38 / 53 us direct against
+      // 32 / 37 / 33 / 36 / 45 us replayed for 1 / 2 / 4 / 8 / 16 steps).
       bool all_large = !pr->steps.empty();
-      for (const Step& st : pr->steps) all_large = all_large && large_gemm(st);
-      pr->graphs = !(g != nullptr && g[0] == '0') && !all_large;
+      size_t launched = 0;
+      for (size_t j = 0; j < pr->steps.size(); ++j) {
+        all_large = all_large && large_gemm(pr->steps[j]);
+        launched += !pr->folded(j) && pr->steps[j].rec.opcode != OP_STEP_COMMIT;
+      }
+      pr->graphs = !(g != nullptr && g[0] == '0') && !all_large && launched > 5;
     }
     *out_program = pr;
     return SHK_HIP_STATUS_OK;

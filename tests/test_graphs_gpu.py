@@ -6,7 +6,8 @@ import pytest
 
 from synaptik_amd.native import HipProgram
 from synaptik_amd.program import ProgramBuilder
-from synaptik_amd.training import Adam, GradientMode, HipTrainingSession, MlpSpec, Sgd, init_parameters
+from synaptik_amd.training import (Adam, GradientMode, HipTrainingSession, MlpSpec, Sgd,
+                                   init_parameters, lower_training_step)
 from tests.conftest import needs_graph_default
 
 pytestmark = pytest.mark.gpu
@@ -68,8 +69,8 @@ def test_graph_replay_accumulation_modes(ctx):
 
 @needs_graph_default
 def test_default_launch_mode_follows_the_program(ctx):
-    """Programs of large GEMMs only launch step by step by default; any other program replays a
-    graph. Either mode gives identical results."""
+    """Programs of large GEMMs only, and programs of at most five launched steps, launch step by
+    step by default; any other program replays a graph. Either mode gives identical results."""
     from synaptik_amd.training import lower_dense_layer
     B, I, O = 1024, 512, 512  # every GEMM 2^28 multiply-adds
     pb, outs = lower_dense_layer(B, I, O, "relu", "in_out")
@@ -90,6 +91,11 @@ def test_default_launch_mode_follows_the_program(ctx):
         assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
     small, _ = lower_dense_layer(64, 32, 32, "relu", "in_out")
     p = HipProgram(ctx, small.image())
+    assert not p.graph_mode()  # three launched steps: direct launches cost less than a replay
+    p.close()
+    spec = MlpSpec.chain([32, 64, 64, 8], hidden="relu", loss="mse")
+    pb, _ = lower_training_step(spec, 64, Sgd(0.1))
+    p = HipProgram(ctx, pb.image())
     assert p.graph_mode()
     p.set_graph_mode(False)
     assert not p.graph_mode()

@@ -14,7 +14,7 @@ from synaptik_amd.program import OP_CE_HEAD, OP_OPTIMIZER, OP_STEP_COMMIT
 from synaptik_amd.training import (Adam, AdamW, Dense, GradientMode, MlpSpec, Sgd,
                                    lower_dense_layer, lower_forward, lower_training_step)
 from tests import plan_hazards as H
-from tests.conftest import needs_two_streams
+from tests.conftest import needs_fold, needs_two_streams
 
 OPTS = [Sgd(0.05), Sgd(0.02, momentum=0.9, nesterov=True, weight_decay=0.01),
         Sgd(0.02, momentum=0.5, dampening=0.2), Adam(1e-3), AdamW(1e-3, 0.9, 0.999, 1e-8, 0.01)]
@@ -78,6 +78,7 @@ def test_runtime_plan_orders_every_conflicting_pair(corpus):
 
 
 @needs_two_streams
+@needs_fold
 def test_folded_steps_have_no_event_edges(corpus):
     """Folded steps are never launched: no step may wait for them (a capture would wait on an
     event never recorded in it) and no later launched step may conflict with them. C3's loss MEAN

@@ -12,7 +12,7 @@ from oracle import oracle
 from synaptik_amd.native import HipArithmeticError, HipIndexError
 from synaptik_amd.training import (Adam, AdamW, Dense, HipTrainingSession, MlpSpec, Sgd,
                                    init_parameters, lower_training_step)
-from tests.conftest import needs_two_streams
+from tests.conftest import needs_fold, needs_two_streams
 
 pytestmark = pytest.mark.gpu
 
@@ -220,6 +220,7 @@ def test_failed_two_stream_steps_leave_no_trace(ctx):
     b.close()
 
 
+@needs_fold
 def test_failure_of_the_folded_bias_update_alone_commits_nothing(ctx):
     """Zero inputs and zero biases make every weight gradient exactly zero (the hidden ReLU is
     off, its gradient masked to zero), while the output bias gradient under MSE SUM, the column

@@ -270,3 +270,24 @@ def test_folded_bias_update_matches_its_own_launch(ctx):
         assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
     a.close()
     b.close()
+
+
+def test_c3_classifier_from_builder_seeded_he_normal_weights(ctx):
+    """The C3 network with the weights bench.py trains: Linear's kaimingReluNormal policy over one
+    L64X128MixRandom per ModelBuilder step (nextGaussian per weight, row-major). Four Adam steps
+    at batch 128 against the oracle from the same initial bytes."""
+    batch = 128
+    spec = MlpSpec.chain([784, 1024, 1024, 10], hidden="relu", loss="ce")
+    Ws, bs = init_parameters(spec, 0, "builder_he_normal")
+    for W, l in zip(Ws, spec.layers):  # He-normal: standard deviation sqrt(2 / fan_in)
+        assert abs(float(W.std()) / np.sqrt(2.0 / l.fan_in) - 1.0) < 0.05
+    rng = np.random.default_rng(3)
+    x = rng.uniform(0, 1, size=(batch, 784)).astype(np.float32)
+    labels = rng.integers(0, 10, size=batch).astype(np.int64)
+    ref = oracle.OracleMLP(Ws, bs, ["relu", "relu", None], "ce",
+                           dict(kind="adam", lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8))
+    sess = HipTrainingSession.open(ctx, spec, Ws, bs, Adam(1e-3, 0.9, 0.999, 1e-8), batch)
+    got = [sess.run(x, labels).objective for _ in range(4)]
+    want = [float(ref.step(x, labels)) for _ in range(4)]
+    np.testing.assert_allclose(got, want, rtol=1e-4)
+    sess.close()

@@ -91,8 +91,14 @@ __device__ __forceinline__ void epilogue_store4(const GemmParams& p, int64_t row
 // column-sum partials) do not depend on CPL: both give identical results.
 constexpr int SK_RB = 4;  // rows per wave batch; SK_RB * 16 <= 64 lanes hold a batch's A values
 constexpr int64_t SMALL_K_NARROW_N = 128;
+// Rows per wave batch: four for 256-column blocks (four columns per lane), one for the narrow
+// form (one column per lane), whose outputs are few: one row per wave gives the epilogue's
+// per-element work (a binary64 tanh, say) four times the waves instead of a serial loop.
+template <int CPL>
+constexpr int small_k_rb() { return CPL == 1 ? 1 : SK_RB; }
 template <int KB, int CPL>
 __global__ void __launch_bounds__(256) gemm_small_k(GemmParams p, int vec_b, int vec_io) {
+  constexpr int RB = small_k_rb<CPL>();
   __shared__ double csum[4][64 * CPL];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t c0 = ((int64_t)blockIdx.x * 64 + lane) * CPL;
@@ -105,7 +111,7 @@ __global__ void __launch_bounds__(256) gemm_small_k(GemmParams p, int vec_b, int
   for (int c = 0; c < CPL; ++c) cs[c] = 0.0;
   // Every lane runs the row loop, also lanes whose columns lie beyond N (their operand reads
   // are clamped into range and they store nothing): the A values of a batch are loaded by
-  // lanes 0 .. SK_RB*KB-1 and read back from them with v_readlane.
+  // lanes 0 .. RB*KB-1 and read back from them with v_readlane.
   {
     float b[KB][CPL];
     const bool full = c0 + 3 < p.N;
@@ -125,30 +131,30 @@ __global__ void __launch_bounds__(256) gemm_small_k(GemmParams p, int vec_b, int
       }
     }
     const int64_t S = (int64_t)gridDim.y * 4;
-    for (int64_t r0 = (int64_t)blockIdx.y * 4 + w; r0 < p.M; r0 += S * SK_RB) {
-      // The batch's SK_RB x KB A values: lane i*KB + k loads A(row i, k) (one load for the
+    for (int64_t r0 = (int64_t)blockIdx.y * 4 + w; r0 < p.M; r0 += S * RB) {
+      // The batch's RB x KB A values: lane i*KB + k loads A(row i, k) (one load for the
       // wave), then every lane reads them back from those lanes (v_readlane into SGPRs).
-      float a[SK_RB][KB];
-      float4 y[SK_RB];
+      float a[RB][KB];
+      float4 y[RB];
       {
         const int i = lane / KB, k = lane - (lane / KB) * KB;
-        const int64_t r = min(r0 + (int64_t)min(i, SK_RB - 1) * S, p.M - 1);
+        const int64_t r = min(r0 + (int64_t)min(i, RB - 1) * S, p.M - 1);
         const int64_t kk = k < K ? k : K - 1;
         const float mine = p.transA ? p.A[kk * p.lda + r] : p.A[r * p.lda + kk];
 #pragma unroll
-        for (int ii = 0; ii < SK_RB; ++ii)
+        for (int ii = 0; ii < RB; ++ii)
 #pragma unroll
           for (int q = 0; q < KB; ++q)
             a[ii][q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), ii * KB + q));
       }
 #pragma unroll
-      for (int i = 0; i < SK_RB; ++i) {
+      for (int i = 0; i < RB; ++i) {
         const int64_t r = min(r0 + i * S, p.M - 1);
         y[i] = (v4 && p.mode == 1) ? *reinterpret_cast<const float4*>(p.aux + r * p.ldaux + c0)
                                    : make_float4(0.f, 0.f, 0.f, 0.f);
       }
 #pragma unroll
-      for (int i = 0; i < SK_RB; ++i) {
+      for (int i = 0; i < RB; ++i) {
         const int64_t r = r0 + i * S;
         if (r >= p.M) break;
         float acc[4];
@@ -347,7 +353,8 @@ bool skinny_enabled() {
 
 int64_t small_k_row_blocks(int64_t M, int64_t N) {
   const int64_t colblocks = (N + 255) / 256;
-  const int64_t rowgroups = (M + 4 * SK_RB - 1) / (4 * SK_RB);  // one row batch per wave
+  const int64_t rb = N <= SMALL_K_NARROW_N ? small_k_rb<1>() : small_k_rb<4>();
+  const int64_t rowgroups = (M + 4 * rb - 1) / (4 * rb);  // one row batch per wave
   const int64_t y = std::min<int64_t>(rowgroups, (1024 + colblocks - 1) / colblocks);
   return std::max<int64_t>(1, std::min<int64_t>(y, SMALL_K_MAX_ROW_BLOCKS));
 }

@@ -341,8 +341,8 @@ def test_skinny_gaussian_within_bound(ctx, shape, ta, tb):
 
 
 @pytest.mark.parametrize("act", ["relu", "tanh", "sigmoid", None])
-@pytest.mark.parametrize("shape", [(1024, 10, 1024), (1, 4096, 512), (300, 16, 12), (5, 37, 3)],
-                         ids=str)
+@pytest.mark.parametrize("shape", [(1024, 10, 1024), (1, 4096, 512), (300, 16, 12), (5, 37, 3),
+                                   (256, 64, 16), (4097, 128, 9)], ids=str)
 def test_skinny_bias_activation_epilogue(ctx, act, shape):
     M, N, K = shape
     rng = np.random.default_rng(23)
@@ -353,8 +353,8 @@ def test_skinny_bias_activation_epilogue(ctx, act, shape):
     assert np.array_equal(Y, oracle.linear_forward(X, W, b, act))
 
 
-@pytest.mark.parametrize("shape", [(1024, 1024, 10), (1000, 1026, 7), (10, 300, 2048), (300, 10, 2048)],
-                         ids=str)
+@pytest.mark.parametrize("shape", [(1024, 1024, 10), (1000, 1026, 7), (10, 300, 2048), (300, 10, 2048),
+                                   (256, 64, 16), (3001, 100, 5), (129, 128, 3)], ids=str)
 def test_skinny_activation_gradient_and_column_sum(ctx, shape):
     M, N, K = shape
     rng = np.random.default_rng(29)

@@ -38,6 +38,9 @@ namespace {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int V2_BK = 32, V2_NT = 256;
+// MFMAs per scheduling group: side work (fragment reads, copies) is issued between groups. Four
+// spreads it finer than eight: 4096^3 launches about 0.3% shorter, the MLP-4096 step 0.3% faster.
+constexpr int V2_GROUP = 4;
 
 template <int BT>
 struct V2Cfg {
@@ -46,7 +49,7 @@ struct V2Cfg {
   static constexpr int TILEF = BT * 32;   // floats per operand per stage
   static constexpr int NI = BT / 32;      // copies per thread per operand per k-tile
   static constexpr int CPR = BT / 4;      // 16-byte chunks per k-row of an M/N-contiguous tile
-  static constexpr int NG = NB * NB / 2;  // groups of 8 MFMAs per half k-tile
+  static constexpr int NG = 4 * NB * NB / V2_GROUP;  // MFMA groups per half k-tile
   static constexpr int CPG = 4 * NI / NG;  // copies issued after a group
   static constexpr int ECPR = WT / 4;     // 16-byte chunks per row of the epilogue transpose
 };
@@ -265,15 +268,15 @@ gemm_f32_v2(GemmParams p) {
     });
   });
 
-  // 4 NB^2 MFMAs of one half-tile in NG groups of 8 (MFMA n: s = n / NB^2, block
+  // 4 NB^2 MFMAs of one half-tile in NG groups of V2_GROUP (MFMA n: s = n / NB^2, block
   // i = (n % NB^2) / NB, j = n % NB, or i and j exchanged for a K-contiguous B); after each group, side(q) issues that group's share of the
   // LDS reads and copies. The scheduling barriers keep this order: reads and copies spread over
   // the MFMA stream instead of stalling it in one place.
   auto mfma_half = [&](const V2Frag<KA, BT>& fa, const V2Frag<KB, BT>& fb, auto side) {
     static_for<NG>([&](auto q) {
       constexpr int Q = decltype(q)::value;
-      static_for<8>([&](auto u) {
-        constexpr int N = 8 * Q + decltype(u)::value;
+      static_for<V2_GROUP>([&](auto u) {
+        constexpr int N = V2_GROUP * Q + decltype(u)::value;
         // (with the operands swapped, consecutive MFMAs share their first operand)
         constexpr int S = N / (NB * NB);
         constexpr int I = KB ? N % NB : (N % (NB * NB)) / NB;

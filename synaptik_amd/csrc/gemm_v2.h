@@ -39,8 +39,10 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int V2_BK = 32, V2_NT = 256;
 // MFMAs per scheduling group: side work (fragment reads, copies) is issued between groups. Four
-// spreads it finer than eight: 4096^3 launches about 0.3% shorter, the MLP-4096 step 0.3% faster.
-constexpr int V2_GROUP = 4;
+// for 128-wide tiles (spreads it finer than eight: 4096^3 launches about 0.3% shorter, the
+// MLP-4096 step 0.3% faster), two for 64-wide tiles (the C3 classifier step about 0.8% faster
+// than with four).
+constexpr int V2_GROUP = 4, V2_GROUP64 = 2;
 
 template <int BT>
 struct V2Cfg {
@@ -49,7 +51,8 @@ struct V2Cfg {
   static constexpr int TILEF = BT * 32;   // floats per operand per stage
   static constexpr int NI = BT / 32;      // copies per thread per operand per k-tile
   static constexpr int CPR = BT / 4;      // 16-byte chunks per k-row of an M/N-contiguous tile
-  static constexpr int NG = 4 * NB * NB / V2_GROUP;  // MFMA groups per half k-tile
+  static constexpr int GS = BT == 64 ? V2_GROUP64 : V2_GROUP;  // MFMAs per group
+  static constexpr int NG = 4 * NB * NB / GS;  // MFMA groups per half k-tile
   static constexpr int CPG = 4 * NI / NG;  // copies issued after a group
   static constexpr int ECPR = WT / 4;     // 16-byte chunks per row of the epilogue transpose
 };
@@ -275,8 +278,8 @@ gemm_f32_v2(GemmParams p) {
   auto mfma_half = [&](const V2Frag<KA, BT>& fa, const V2Frag<KB, BT>& fb, auto side) {
     static_for<NG>([&](auto q) {
       constexpr int Q = decltype(q)::value;
-      static_for<V2_GROUP>([&](auto u) {
-        constexpr int N = V2_GROUP * Q + decltype(u)::value;
+      static_for<Cfg::GS>([&](auto u) {
+        constexpr int N = Cfg::GS * Q + decltype(u)::value;
         // (with the operands swapped, consecutive MFMAs share their first operand)
         constexpr int S = N / (NB * NB);
         constexpr int I = KB ? N % NB : (N % (NB * NB)) / NB;
